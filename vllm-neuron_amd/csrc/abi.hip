@@ -1,0 +1,337 @@
+// abi.hip — the extern "C" boundary: argument validation (mirroring the
+// reference's ValueError / NotImplementedError checks), thread-local error
+// reporting and dispatch to the kernel launchers.
+#include <stdint.h>
+
+#include <cstdio>
+#include <string>
+
+#include "mia_device.h"
+#include "mia_internal.h"
+
+namespace mia {
+
+static thread_local std::string g_last_error;
+
+int set_error(int code, const std::string &msg) {
+  g_last_error = msg;
+  return code;
+}
+
+int check_hip(hipError_t err, const char *what) {
+  if (err == hipSuccess) return MIA_OK;
+  return set_error(MIA_ERR_RUNTIME,
+                   std::string(what) + ": " + hipGetErrorString(err));
+}
+
+}  // namespace mia
+
+using mia::set_error;
+
+#define MIA_REQUIRE(cond, code, msg)          \
+  do {                                        \
+    if (!(cond)) return set_error(code, msg); \
+  } while (0)
+
+static bool aligned(const void *p, size_t a) {
+  return ((uintptr_t)p % a) == 0;
+}
+
+extern "C" {
+
+int mia_abi_version(void) { return MIA_ABI_VERSION; }
+
+const char *mia_last_error(void) { return mia::g_last_error.c_str(); }
+
+size_t mia_args_size(int which) {
+  switch (which) {
+    case 0: return sizeof(mia_kv_write_args);
+    case 1: return sizeof(mia_gather_args);
+    case 2: return sizeof(mia_mask_args);
+    case 3: return sizeof(mia_decode_args);
+    case 4: return sizeof(mia_prefill_args);
+    case 5: return sizeof(mia_slot_mapping_args);
+    case 6: return sizeof(mia_packed_k_args);
+    case 7: return sizeof(mia_swa_trim_args);
+    case 8: return sizeof(mia_scatter_rows_args);
+    default: return 0;
+  }
+}
+
+int mia_kv_write(const mia_kv_write_args *a, mia_stream_t stream) {
+  mia::g_last_error.clear();
+  MIA_REQUIRE(a, MIA_ERR_VALUE, "kv_write: null args");
+  MIA_REQUIRE(a->num_tokens >= 0, MIA_ERR_VALUE, "kv_write: num_tokens < 0");
+  if (a->num_tokens == 0) return MIA_OK;
+  MIA_REQUIRE(a->k_src && a->slots && a->k_cache, MIA_ERR_VALUE,
+              "kv_write: null tensor pointer");
+  MIA_REQUIRE(!a->v_src || a->v_cache, MIA_ERR_VALUE,
+              "kv_write: v_src given without v_cache");
+  MIA_REQUIRE(a->src_dtype == MIA_DTYPE_BF16 || a->src_dtype == MIA_DTYPE_F16 ||
+                  a->src_dtype == MIA_DTYPE_F32,
+              MIA_ERR_NOT_IMPLEMENTED, "kv_write: source dtype must be bf16/f16/f32");
+  MIA_REQUIRE(a->slot_dtype == MIA_DTYPE_I32 || a->slot_dtype == MIA_DTYPE_I64 ||
+                  a->slot_dtype == MIA_DTYPE_U32,
+              MIA_ERR_VALUE, "kv_write: slot dtype must be int32/int64/uint32");
+  MIA_REQUIRE(a->cache_dtype == MIA_DTYPE_BF16 || a->cache_dtype == MIA_DTYPE_F16 ||
+                  a->cache_dtype == MIA_DTYPE_F32 ||
+                  a->cache_dtype == MIA_DTYPE_FP8_E4M3FN,
+              MIA_ERR_NOT_IMPLEMENTED, "kv_write: unsupported cache dtype");
+  MIA_REQUIRE(a->num_blocks > 0 && a->block_size > 0 && a->num_kv_heads > 0 &&
+                  a->head_dim > 0,
+              MIA_ERR_VALUE, "kv_write: bad cache geometry");
+  MIA_REQUIRE(!a->k_packed || (a->block_size % 2 == 0 &&
+                               a->cache_dtype == MIA_DTYPE_FP8_E4M3FN),
+              MIA_ERR_VALUE,
+              "kv_write: packed K needs an even block_size and an fp8 cache");
+  if (a->quant_mode != MIA_QUANT_NONE) {
+    MIA_REQUIRE(a->cache_dtype == MIA_DTYPE_FP8_E4M3FN, MIA_ERR_VALUE,
+                "kv_write: quantisation requires an fp8 cache");
+    MIA_REQUIRE(a->k_scale && (!a->v_src || a->v_scale), MIA_ERR_VALUE,
+                "kv_write: quant scales missing");
+    MIA_REQUIRE(a->quant_mode >= MIA_QUANT_MUL_BF16 &&
+                    a->quant_mode <= MIA_QUANT_DIV_F32,
+                MIA_ERR_VALUE, "kv_write: bad quant mode");
+  }
+  return mia::launch_kv_write(*a, (hipStream_t)stream);
+}
+
+int mia_gather_kv(const mia_gather_args *a, mia_stream_t stream) {
+  mia::g_last_error.clear();
+  MIA_REQUIRE(a && a->cache && a->block_table && a->out, MIA_ERR_VALUE,
+              "gather: null pointer");
+  MIA_REQUIRE(a->batch >= 0 && a->num_kv_heads > 0 && a->blocks_per_seq >= 0 &&
+                  a->block_size > 0 && a->head_dim > 0,
+              MIA_ERR_VALUE, "gather: bad geometry");
+  return mia::launch_gather(*a, (hipStream_t)stream);
+}
+
+int mia_decode_mask(const mia_mask_args *a, mia_stream_t stream) {
+  mia::g_last_error.clear();
+  MIA_REQUIRE(a && a->out, MIA_ERR_VALUE, "decode_mask: null pointer");
+  MIA_REQUIRE(a->bs >= 0 && a->q_head >= 0 && a->s_active > 0 && a->s_prior >= 0,
+              MIA_ERR_VALUE, "decode_mask: bad geometry");
+  MIA_REQUIRE(a->s_prior % 128 == 0, MIA_ERR_VALUE,
+              "s_prior must be divisible by 128");
+  MIA_REQUIRE(a->local_filled || a->pos_ids, MIA_ERR_VALUE,
+              "decode_mask: pos_ids missing");
+  return mia::launch_decode_mask(*a, (hipStream_t)stream);
+}
+
+static int validate_decode(const mia_decode_args *a) {
+  MIA_REQUIRE(a, MIA_ERR_VALUE, "decode: null args");
+  MIA_REQUIRE(a->q && a->k_new && a->v_new && a->k_cache && a->v_cache &&
+                  a->block_table && a->out,
+              MIA_ERR_VALUE, "decode: null tensor pointer");
+  MIA_REQUIRE(a->batch > 0 && a->s_active > 0 && a->num_q_heads > 0 &&
+                  a->num_kv_heads > 0,
+              MIA_ERR_VALUE, "decode: bad shape");
+  MIA_REQUIRE(a->num_q_heads % a->num_kv_heads == 0, MIA_ERR_VALUE,
+              "GQA requires q_heads divisible by kv_heads");
+  MIA_REQUIRE(a->head_dim == 64 || a->head_dim == 128, MIA_ERR_NOT_IMPLEMENTED,
+              "decode: head_dim must be 64 or 128");
+  MIA_REQUIRE(a->cache_dtype == MIA_DTYPE_BF16 ||
+                  a->cache_dtype == MIA_DTYPE_FP8_E4M3FN,
+              MIA_ERR_NOT_IMPLEMENTED, "decode: cache dtype must be bf16 or fp8");
+  MIA_REQUIRE(!a->k_packed, MIA_ERR_NOT_IMPLEMENTED,
+              "decode: packed K is read through an unpacked view");
+  MIA_REQUIRE(a->block_size > 0 && a->block_size % 16 == 0,
+              MIA_ERR_NOT_IMPLEMENTED, "decode: block_size must be a multiple of 16");
+  MIA_REQUIRE(a->num_blocks > 0 && a->blocks_per_seq > 0, MIA_ERR_VALUE,
+              "decode: empty cache or table");
+  const int64_t s_ctx = (int64_t)a->blocks_per_seq * a->block_size;
+  MIA_REQUIRE(s_ctx >= a->s_active, MIA_ERR_VALUE,
+              "decode: table span shorter than the active tokens");
+  MIA_REQUIRE(s_ctx < (1ll << 24), MIA_ERR_VALUE,
+              "decode: context beyond 2^24 tokens");
+  const int G = a->num_q_heads / a->num_kv_heads;
+  MIA_REQUIRE(G * a->s_active <= 64 && a->s_active <= 16,
+              MIA_ERR_NOT_IMPLEMENTED,
+              "decode: at most 16 active tokens and 64 query columns per kv head");
+  MIA_REQUIRE(a->mask_mode == 0 || a->mask_mode == 1, MIA_ERR_VALUE,
+              "decode: bad mask mode");
+  if (a->mask_mode == 0)
+    MIA_REQUIRE(a->pos_ids, MIA_ERR_VALUE, "decode: pos_ids missing");
+  else
+    MIA_REQUIRE(a->full_mask, MIA_ERR_VALUE, "decode: mask missing");
+  const int eb = a->cache_dtype == MIA_DTYPE_FP8_E4M3FN ? 1 : 2;
+  const size_t vec = a->cache_dtype == MIA_DTYPE_FP8_E4M3FN ? 8 : 16;
+  MIA_REQUIRE(a->k_cache_stride[3] == 1 && a->v_cache_stride[3] == 1,
+              MIA_ERR_VALUE, "decode: cache head_dim must be contiguous");
+  MIA_REQUIRE(aligned(a->k_cache, vec) && aligned(a->v_cache, vec),
+              MIA_ERR_VALUE, "decode: cache pointers must be vector aligned");
+  for (int i = 0; i < 3; ++i)
+    MIA_REQUIRE(((a->k_cache_stride[i] * eb) % vec == 0) &&
+                    ((a->v_cache_stride[i] * eb) % vec == 0),
+                MIA_ERR_VALUE, "decode: cache strides must be vector aligned");
+  MIA_REQUIRE(a->q_stride[3] == 1 && aligned(a->q, 16) &&
+                  (a->q_stride[0] * 2) % 16 == 0 && (a->q_stride[1] * 2) % 16 == 0 &&
+                  (a->q_stride[2] * 2) % 16 == 0,
+              MIA_ERR_VALUE, "decode: q must be 16-byte aligned with contiguous d");
+  MIA_REQUIRE(a->k_new_stride[3] == 1 && a->v_new_stride[3] == 1, MIA_ERR_VALUE,
+              "decode: new K/V head_dim must be contiguous");
+  MIA_REQUIRE(a->out_dtype == MIA_DTYPE_BF16, MIA_ERR_NOT_IMPLEMENTED,
+              "decode: output dtype must be bf16");
+  if (a->quant_mode != MIA_QUANT_NONE) {
+    MIA_REQUIRE(a->cache_dtype == MIA_DTYPE_FP8_E4M3FN && a->k_quant && a->v_quant,
+                MIA_ERR_VALUE,
+                "decode: active-row quantisation needs an fp8 cache and both scales");
+  }
+  return MIA_OK;
+}
+
+size_t mia_decode_workspace_bytes(const mia_decode_args *a) {
+  mia::g_last_error.clear();
+  if (validate_decode(a) != MIA_OK) return 0;
+  return mia::plan_decode(*a).ws_bytes;
+}
+
+int mia_paged_decode(const mia_decode_args *a, mia_stream_t stream) {
+  mia::g_last_error.clear();
+  int rc = validate_decode(a);
+  if (rc) return rc;
+  mia::DecodePlan pl = mia::plan_decode(*a);
+  MIA_REQUIRE(a->workspace && a->workspace_bytes >= pl.ws_bytes, MIA_ERR_VALUE,
+              "decode: workspace too small (query mia_decode_workspace_bytes)");
+  MIA_REQUIRE(aligned(a->workspace, 256), MIA_ERR_VALUE,
+              "decode: workspace must be 256-byte aligned");
+  return mia::launch_paged_decode(*a, pl, (hipStream_t)stream);
+}
+
+int mia_paged_prefill(const mia_prefill_args *a, mia_stream_t stream) {
+  mia::g_last_error.clear();
+  MIA_REQUIRE(a, MIA_ERR_VALUE, "prefill: null args");
+  if (a->num_seqs == 0) return MIA_OK;
+  MIA_REQUIRE(a->q && a->cu_seqlens_q && a->prior_tokens && a->k_cache &&
+                  a->v_cache && a->block_table && a->out,
+              MIA_ERR_VALUE, "prefill: null tensor pointer");
+  MIA_REQUIRE(a->num_q_heads > 0 && a->num_kv_heads > 0 &&
+                  a->num_q_heads % a->num_kv_heads == 0,
+              MIA_ERR_VALUE, "GQA requires q_heads divisible by kv_heads");
+  MIA_REQUIRE(a->head_dim == 64 || a->head_dim == 128, MIA_ERR_NOT_IMPLEMENTED,
+              "prefill: head_dim must be 64 or 128");
+  MIA_REQUIRE(a->cache_dtype == MIA_DTYPE_BF16 ||
+                  a->cache_dtype == MIA_DTYPE_FP8_E4M3FN,
+              MIA_ERR_NOT_IMPLEMENTED, "prefill: cache dtype must be bf16 or fp8");
+  MIA_REQUIRE(!a->k_packed, MIA_ERR_NOT_IMPLEMENTED,
+              "prefill: packed K is read through an unpacked view");
+  MIA_REQUIRE(a->block_size > 0 && a->num_blocks > 0 && a->blocks_per_seq >= 0,
+              MIA_ERR_VALUE, "prefill: bad cache geometry");
+  MIA_REQUIRE(a->sliding_window >= 0, MIA_ERR_VALUE, "prefill: negative window");
+  const int eb = a->cache_dtype == MIA_DTYPE_FP8_E4M3FN ? 1 : 2;
+  const size_t vec = a->cache_dtype == MIA_DTYPE_FP8_E4M3FN ? 8 : 16;
+  MIA_REQUIRE(a->k_cache_stride[3] == 1 && a->v_cache_stride[3] == 1,
+              MIA_ERR_VALUE, "prefill: cache head_dim must be contiguous");
+  MIA_REQUIRE(aligned(a->k_cache, vec) && aligned(a->v_cache, vec),
+              MIA_ERR_VALUE, "prefill: cache pointers must be vector aligned");
+  for (int i = 0; i < 3; ++i)
+    MIA_REQUIRE(((a->k_cache_stride[i] * eb) % vec == 0) &&
+                    ((a->v_cache_stride[i] * eb) % vec == 0),
+                MIA_ERR_VALUE, "prefill: cache strides must be vector aligned");
+  MIA_REQUIRE(a->q_stride[2] == 1 && aligned(a->q, 16) &&
+                  (a->q_stride[0] * 2) % 16 == 0 && (a->q_stride[1] * 2) % 16 == 0,
+              MIA_ERR_VALUE, "prefill: q must be 16-byte aligned with contiguous d");
+  MIA_REQUIRE(a->out_dtype == MIA_DTYPE_BF16 && a->out_stride[2] == 1 &&
+                  aligned(a->out, 8) && (a->out_stride[0] * 2) % 8 == 0 &&
+                  (a->out_stride[1] * 2) % 8 == 0,
+              MIA_ERR_VALUE, "prefill: output must be bf16 with contiguous d");
+  MIA_REQUIRE(a->max_seqlen_q >= 0, MIA_ERR_VALUE, "prefill: max_seqlen_q < 0");
+  return mia::launch_paged_prefill(*a, (hipStream_t)stream);
+}
+
+static void slot_mapping_one(const mia_slot_mapping_args *a, int64_t t) {
+  const int64_t pos = a->positions[t];
+  const int64_t req = a->req_indices[t];
+  const int64_t W = a->cp_world_size;
+  const int64_t vbs = (int64_t)a->block_size * W;
+  const int32_t bnum = a->block_table[req * a->bt_row_stride + pos / vbs];
+  const int32_t base = (int32_t)((uint32_t)bnum * (uint32_t)a->block_size);
+  int64_t slot;
+  if (W > 1) {
+    const int64_t I = a->cp_interleave;
+    const int64_t voff = pos % vbs;
+    const bool local = ((voff / I) % W) == a->cp_rank;
+    const int64_t boff = voff / (W * I) * I + voff % I;
+    slot = local ? (int64_t)base + boff : (int64_t)a->null_slot;
+  } else {
+    slot = (int64_t)base + pos % a->block_size;
+  }
+  a->slot_mapping[t] = slot;
+}
+
+static int validate_slot_mapping(const mia_slot_mapping_args *a) {
+  MIA_REQUIRE(a && a->block_table && a->positions && a->req_indices &&
+                  a->slot_mapping,
+              MIA_ERR_VALUE, "slot_mapping: null pointer");
+  MIA_REQUIRE(a->block_size > 0 && a->cp_world_size >= 1 &&
+                  (a->cp_world_size == 1 || a->cp_interleave > 0),
+              MIA_ERR_VALUE, "slot_mapping: bad geometry");
+  return MIA_OK;
+}
+
+int mia_slot_mapping(const mia_slot_mapping_args *a, mia_stream_t stream) {
+  mia::g_last_error.clear();
+  int rc = validate_slot_mapping(a);
+  if (rc) return rc;
+  return mia::launch_slot_mapping(*a, (hipStream_t)stream);
+}
+
+int mia_slot_mapping_host(const mia_slot_mapping_args *a) {
+  mia::g_last_error.clear();
+  int rc = validate_slot_mapping(a);
+  if (rc) return rc;
+  for (int64_t t = 0; t < a->num_tokens; ++t) {
+    const int64_t pos = a->positions[t];
+    const int64_t req = a->req_indices[t];
+    MIA_REQUIRE(pos >= 0 && req >= 0, MIA_ERR_VALUE,
+                "slot_mapping: negative position or request index");
+    MIA_REQUIRE(pos / ((int64_t)a->block_size * a->cp_world_size) <
+                    a->max_blocks_per_req,
+                MIA_ERR_VALUE, "slot_mapping: position beyond the block table");
+    slot_mapping_one(a, t);
+  }
+  return MIA_OK;
+}
+
+int mia_remap_null_block(const int32_t *in, int32_t *out, int64_t n,
+                         int32_t null_block, mia_stream_t stream) {
+  mia::g_last_error.clear();
+  MIA_REQUIRE(in && out, MIA_ERR_VALUE, "remap_null_block: null pointer");
+  return mia::launch_remap_null(in, out, n, null_block, (hipStream_t)stream);
+}
+
+int mia_swa_trim(const mia_swa_trim_args *a, mia_stream_t stream) {
+  mia::g_last_error.clear();
+  MIA_REQUIRE(a && a->block_table && a->ctx_lens && a->out_table && a->pos_offset,
+              MIA_ERR_VALUE, "swa_trim: null pointer");
+  MIA_REQUIRE(a->num_swa_blocks > 0 && a->block_size > 0 && a->num_reqs >= 0,
+              MIA_ERR_VALUE, "swa_trim: bad geometry");
+  return mia::launch_swa_trim(*a, (hipStream_t)stream);
+}
+
+int mia_packed_k_convert(const mia_packed_k_args *a, mia_stream_t stream) {
+  mia::g_last_error.clear();
+  MIA_REQUIRE(a && a->src && a->dst, MIA_ERR_VALUE, "packed_k: null pointer");
+  MIA_REQUIRE(a->block_len % 2 == 0, MIA_ERR_VALUE,
+              "block_len must be even to pack");
+  MIA_REQUIRE(a->elem_bytes == 1 || a->elem_bytes == 2, MIA_ERR_VALUE,
+              "packed_k: element size must be 1 or 2 bytes");
+  MIA_REQUIRE(a->direction == 0 || a->direction == 1, MIA_ERR_VALUE,
+              "packed_k: bad direction");
+  return mia::launch_packed_k(*a, (hipStream_t)stream);
+}
+
+int mia_scatter_rows(const mia_scatter_rows_args *a, mia_stream_t stream) {
+  mia::g_last_error.clear();
+  MIA_REQUIRE(a && a->src && a->cache && a->block_idx && a->head_idx && a->pos_idx,
+              MIA_ERR_VALUE, "scatter_rows: null pointer");
+  MIA_REQUIRE(a->elem_bytes == 1 || a->elem_bytes == 2 || a->elem_bytes == 4,
+              MIA_ERR_VALUE, "scatter_rows: element size must be 1, 2 or 4 bytes");
+  MIA_REQUIRE(!a->pair_mode || (a->k_packed && a->num_rows % 2 == 0), MIA_ERR_VALUE,
+              "scatter_rows: pair mode needs a packed cache and an even row count");
+  MIA_REQUIRE(a->num_rows >= 0 && a->head_dim > 0, MIA_ERR_VALUE,
+              "scatter_rows: bad geometry");
+  return mia::launch_scatter_rows(*a, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,310 @@
+// kv_cache.hip — integer / byte kernels around the paged KV cache:
+//   * kv_write      : scatter new K/V rows to their slots (bf16 copy or FP8
+//                     quantise), sentinel slots skipped
+//   * gather        : block-table gather of the padded context (parity/debug)
+//   * packed_k      : swizzle / unswizzle of the packed FP8 K layout
+//   * slot_mapping  : slot = bt[req, pos // bs] * bs + pos % bs (+ DCP variant)
+//   * remap_null    : block-table 0 -> -1
+//   * swa_trim      : sliding-window decode table trim + position offset
+// All are HBM-bound element kernels; each thread owns whole 16-byte chunks
+// where the layout allows it.
+#include "mia_device.h"
+#include "mia_internal.h"
+
+namespace mia {
+namespace {
+
+// ---------------------------------------------------------------------------
+// element load / store by dtype
+// ---------------------------------------------------------------------------
+MIA_DEV float load_as_f32(const void *base, int64_t idx, int dtype) {
+  if (dtype == MIA_DTYPE_BF16)
+    return bf16_bits_to_f32(((const uint16_t *)base)[idx]);
+  if (dtype == MIA_DTYPE_F16)
+    return __half2float(((const __half *)base)[idx]);
+  return ((const float *)base)[idx];
+}
+
+MIA_DEV int64_t load_slot(const void *slots, int64_t t, int dtype) {
+  if (dtype == MIA_DTYPE_I64) return ((const int64_t *)slots)[t];
+  if (dtype == MIA_DTYPE_U32) return (int64_t)((const uint32_t *)slots)[t];
+  return (int64_t)((const int32_t *)slots)[t];
+}
+
+// Stores x (already an exact value of the source dtype) into a cache element.
+MIA_DEV void store_cache(void *cache, int64_t idx, int cache_dtype,
+                         int src_dtype, uint32_t src_bits, float x, float s,
+                         int qmode) {
+  if (cache_dtype == MIA_DTYPE_BF16) {
+    uint16_t v = (src_dtype == MIA_DTYPE_BF16) ? (uint16_t)src_bits
+                                               : (uint16_t)f32_to_bf16_bits(x);
+    ((uint16_t *)cache)[idx] = v;
+  } else if (cache_dtype == MIA_DTYPE_F16) {
+    ((__half *)cache)[idx] = __float2half_rn(x);
+  } else if (cache_dtype == MIA_DTYPE_F32) {
+    ((float *)cache)[idx] = x;
+  } else {  // FP8 e4m3fn
+    uint32_t code = (qmode == MIA_QUANT_NONE) ? f32_to_e4m3fn_bits(x)
+                                              : quantize_e4m3fn(x, s, qmode);
+    ((uint8_t *)cache)[idx] = (uint8_t)code;
+  }
+}
+
+// One workgroup per (token, head) row pair; threads walk head_dim.
+__global__ void kv_write_kernel(mia_kv_write_args a) {
+  const int64_t row = blockIdx.x;  // token * Hkv + head
+  const int64_t t = row / a.num_kv_heads;
+  const int h = (int)(row % a.num_kv_heads);
+  const int64_t max_slot = (int64_t)a.num_blocks * a.block_size;
+  const int64_t slot = load_slot(a.slots, t, a.slot_dtype);
+  if (slot < 0 || slot >= max_slot) return;  // sentinel: skipped
+  const int64_t blk = slot / a.block_size;
+  const int64_t off = slot % a.block_size;
+  float ks = 1.0f, vs = 1.0f;
+  if (a.quant_mode != MIA_QUANT_NONE) {
+    ks = a.k_scale[a.scale_per_head ? h : 0];
+    if (a.v_scale) vs = a.v_scale[a.scale_per_head ? h : 0];
+  }
+  int64_t kdst;
+  if (a.k_packed) {
+    kdst = blk * a.k_cache_stride[0] + h * a.k_cache_stride[1] +
+           (off >> 1) * a.k_cache_stride[2] + (off & 1) * a.k_cache_stride[4];
+  } else {
+    kdst = blk * a.k_cache_stride[0] + h * a.k_cache_stride[1] +
+           off * a.k_cache_stride[2];
+  }
+  const int64_t vdst = blk * a.v_cache_stride[0] + h * a.v_cache_stride[1] +
+                       off * a.v_cache_stride[2];
+  const int64_t ksrc = t * a.k_src_stride[0] + h * a.k_src_stride[1];
+  const int64_t vsrc = t * a.v_src_stride[0] + h * a.v_src_stride[1];
+  for (int e = threadIdx.x; e < a.head_dim; e += blockDim.x) {
+    {
+      const int64_t si = ksrc + e * a.k_src_stride[2];
+      uint32_t bits = (a.src_dtype == MIA_DTYPE_BF16)
+                          ? ((const uint16_t *)a.k_src)[si] : 0u;
+      float x = load_as_f32(a.k_src, si, a.src_dtype);
+      store_cache(a.k_cache, kdst + e * a.k_cache_stride[3], a.cache_dtype,
+                  a.src_dtype, bits, x, ks, a.quant_mode);
+    }
+    if (a.v_src) {
+      const int64_t si = vsrc + e * a.v_src_stride[2];
+      uint32_t bits = (a.src_dtype == MIA_DTYPE_BF16)
+                          ? ((const uint16_t *)a.v_src)[si] : 0u;
+      float x = load_as_f32(a.v_src, si, a.src_dtype);
+      store_cache(a.v_cache, vdst + e * a.v_cache_stride[3], a.cache_dtype,
+                  a.src_dtype, bits, x, vs, a.quant_mode);
+    }
+  }
+}
+
+MIA_DEV int elem_bytes(int dtype) {
+  return dtype == MIA_DTYPE_FP8_E4M3FN ? 1 : (dtype == MIA_DTYPE_F32 ? 4 : 2);
+}
+
+// out[b, h, j*bs + t, e] = cache[max(bt[b,h,j], 0), h, t, e]
+__global__ void gather_kernel(mia_gather_args a, int64_t total) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  const int64_t s_ctx = (int64_t)a.blocks_per_seq * a.block_size;
+  const int e = (int)(i % a.head_dim);
+  int64_t r = i / a.head_dim;
+  const int64_t pos = r % s_ctx;
+  r /= s_ctx;
+  const int h = (int)(r % a.num_kv_heads);
+  const int64_t b = r / a.num_kv_heads;
+  const int64_t j = pos / a.block_size;
+  const int64_t t = pos % a.block_size;
+  int32_t blk = a.block_table[b * a.bt_stride[0] + h * a.bt_stride[1] +
+                              j * a.bt_stride[2]];
+  if (blk < 0) blk = 0;  // the reference clamps -1 to block 0
+  int64_t src;
+  if (a.k_packed) {
+    src = blk * a.cache_stride[0] + h * a.cache_stride[1] +
+          (t >> 1) * a.cache_stride[2] + e * a.cache_stride[3] +
+          (t & 1) * a.cache_stride[4];
+  } else {
+    src = blk * a.cache_stride[0] + h * a.cache_stride[1] +
+          t * a.cache_stride[2] + e * a.cache_stride[3];
+  }
+  const int eb = elem_bytes(a.cache_dtype);
+  if (eb == 1) ((uint8_t *)a.out)[i] = ((const uint8_t *)a.cache)[src];
+  else if (eb == 2) ((uint16_t *)a.out)[i] = ((const uint16_t *)a.cache)[src];
+  else ((uint32_t *)a.out)[i] = ((const uint32_t *)a.cache)[src];
+}
+
+// Packed K permutation on contiguous tensors.
+// unpacked [n, bl, d]  <->  packed [n, bl/2, d, 2]
+template <typename T>
+__global__ void packed_k_kernel(const T *__restrict__ src, T *__restrict__ dst,
+                                int64_t total, int bl, int d, int direction) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= total) return;
+  // i indexes the destination tensor.
+  const int64_t per = (int64_t)bl * d;
+  const int64_t n = i / per;
+  const int64_t w = i % per;
+  int64_t s;
+  if (direction == 0) {  // dst packed: w = (t2 * d + e) * 2 + lane
+    const int64_t lane = w & 1;
+    const int64_t e = (w >> 1) % d;
+    const int64_t t2 = (w >> 1) / d;
+    s = n * per + (t2 * 2 + lane) * d + e;
+  } else {  // dst unpacked: w = t * d + e
+    const int64_t t = w / d;
+    const int64_t e = w % d;
+    s = n * per + ((t >> 1) * d + e) * 2 + (t & 1);
+  }
+  dst[i] = src[s];
+}
+
+__global__ void scatter_rows_kernel(mia_scatter_rows_args a) {
+  const int64_t r = blockIdx.x;
+  int64_t src_row = r, lane = 0, rep = r;
+  if (a.pair_mode) {
+    rep = r & ~(int64_t)1;
+    lane = r & 1;
+  }
+  const int64_t blk = a.block_idx[rep];
+  const int64_t h = a.head_idx[rep];
+  const int64_t pos = a.pos_idx[rep];
+  if (blk < 0 || blk >= a.num_blocks || h < 0 || h >= a.num_kv_heads || pos < 0 ||
+      pos >= a.block_size)
+    return;
+  int64_t dst;
+  if (a.k_packed) {
+    const int64_t t = a.pair_mode ? ((pos >> 1) << 1) + lane : pos;
+    dst = blk * a.cache_stride[0] + h * a.cache_stride[1] + (t >> 1) * a.cache_stride[2] +
+          (t & 1) * a.cache_stride[4];
+  } else {
+    dst = blk * a.cache_stride[0] + h * a.cache_stride[1] + pos * a.cache_stride[2];
+  }
+  const int64_t src = src_row * a.src_row_stride;
+  for (int e = threadIdx.x; e < a.head_dim; e += blockDim.x) {
+    const int64_t di = dst + e * a.cache_stride[3];
+    if (a.elem_bytes == 1)
+      ((uint8_t *)a.cache)[di] = ((const uint8_t *)a.src)[src + e];
+    else if (a.elem_bytes == 2)
+      ((uint16_t *)a.cache)[di] = ((const uint16_t *)a.src)[src + e];
+    else
+      ((uint32_t *)a.cache)[di] = ((const uint32_t *)a.src)[src + e];
+  }
+}
+
+__global__ void slot_mapping_kernel(mia_slot_mapping_args a) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= a.num_tokens) return;
+  const int64_t pos = a.positions[t];
+  const int64_t req = a.req_indices[t];
+  const int64_t W = a.cp_world_size;
+  const int64_t vbs = (int64_t)a.block_size * W;
+  const int64_t bidx = pos / vbs;
+  // int32 table entry times block_size stays int32 in the reference
+  // (numpy int32 * int), then widens when added to the int64 offset.
+  const int32_t bnum = a.block_table[req * a.bt_row_stride + bidx];
+  const int32_t base = (int32_t)((uint32_t)bnum * (uint32_t)a.block_size);
+  int64_t slot;
+  if (W > 1) {
+    const int64_t I = a.cp_interleave;
+    const int64_t voff = pos % vbs;
+    const bool local = ((voff / I) % W) == a.cp_rank;
+    const int64_t boff = voff / (W * I) * I + voff % I;
+    slot = local ? (int64_t)base + boff : (int64_t)a.null_slot;
+  } else {
+    slot = (int64_t)base + pos % a.block_size;
+  }
+  a.slot_mapping[t] = slot;
+}
+
+__global__ void remap_null_kernel(const int32_t *in, int32_t *out, int64_t n,
+                                  int32_t null_block) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int32_t v = in[i];
+  out[i] = (v == null_block) ? -1 : v;
+}
+
+__global__ void swa_trim_kernel(mia_swa_trim_args a) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)a.num_reqs * a.num_swa_blocks;
+  if (i >= total) return;
+  const int64_t r = i / a.num_swa_blocks;
+  const int64_t j = i % a.num_swa_blocks;
+  int64_t start = a.ctx_lens[r] / a.block_size - a.num_swa_blocks + 1;
+  if (start < 0) start = 0;
+  const int64_t col = start + j;
+  a.out_table[i] = (col < a.bt_width) ? a.block_table[r * a.bt_row_stride + col]
+                                      : -1;
+  if (j == 0) a.pos_offset[r] = (int32_t)(start * a.block_size);
+}
+
+inline unsigned grid_for(int64_t n, int threads) {
+  return (unsigned)((n + threads - 1) / threads);
+}
+
+}  // namespace
+
+int launch_kv_write(const mia_kv_write_args &a, hipStream_t s) {
+  const int64_t rows = a.num_tokens * a.num_kv_heads;
+  if (rows == 0) return MIA_OK;
+  int threads = a.head_dim >= 128 ? 128 : 64;
+  hipLaunchKernelGGL(kv_write_kernel, dim3((unsigned)rows), dim3(threads), 0,
+                     s, a);
+  return check_hip(hipGetLastError(), "kv_write launch");
+}
+
+int launch_gather(const mia_gather_args &a, hipStream_t s) {
+  const int64_t total = (int64_t)a.batch * a.num_kv_heads * a.blocks_per_seq *
+                        a.block_size * a.head_dim;
+  if (total == 0) return MIA_OK;
+  hipLaunchKernelGGL(gather_kernel, dim3(grid_for(total, 256)), dim3(256), 0,
+                     s, a, total);
+  return check_hip(hipGetLastError(), "gather launch");
+}
+
+int launch_packed_k(const mia_packed_k_args &a, hipStream_t s) {
+  const int64_t total = a.n_rows * a.block_len * a.head_dim;
+  if (total == 0) return MIA_OK;
+  if (a.elem_bytes == 1) {
+    hipLaunchKernelGGL(packed_k_kernel<uint8_t>, dim3(grid_for(total, 256)),
+                       dim3(256), 0, s, (const uint8_t *)a.src,
+                       (uint8_t *)a.dst, total, a.block_len, a.head_dim,
+                       a.direction);
+  } else {
+    hipLaunchKernelGGL(packed_k_kernel<uint16_t>, dim3(grid_for(total, 256)),
+                       dim3(256), 0, s, (const uint16_t *)a.src,
+                       (uint16_t *)a.dst, total, a.block_len, a.head_dim,
+                       a.direction);
+  }
+  return check_hip(hipGetLastError(), "packed_k launch");
+}
+
+int launch_scatter_rows(const mia_scatter_rows_args &a, hipStream_t s) {
+  if (a.num_rows == 0) return MIA_OK;
+  hipLaunchKernelGGL(scatter_rows_kernel, dim3((unsigned)a.num_rows), dim3(64), 0, s, a);
+  return check_hip(hipGetLastError(), "scatter_rows launch");
+}
+
+int launch_slot_mapping(const mia_slot_mapping_args &a, hipStream_t s) {
+  if (a.num_tokens == 0) return MIA_OK;
+  hipLaunchKernelGGL(slot_mapping_kernel, dim3(grid_for(a.num_tokens, 256)),
+                     dim3(256), 0, s, a);
+  return check_hip(hipGetLastError(), "slot_mapping launch");
+}
+
+int launch_remap_null(const int32_t *in, int32_t *out, int64_t n,
+                      int32_t null_block, hipStream_t s) {
+  if (n == 0) return MIA_OK;
+  hipLaunchKernelGGL(remap_null_kernel, dim3(grid_for(n, 256)), dim3(256), 0,
+                     s, in, out, n, null_block);
+  return check_hip(hipGetLastError(), "remap_null launch");
+}
+
+int launch_swa_trim(const mia_swa_trim_args &a, hipStream_t s) {
+  const int64_t total = (int64_t)a.num_reqs * a.num_swa_blocks;
+  if (total == 0) return MIA_OK;
+  hipLaunchKernelGGL(swa_trim_kernel, dim3(grid_for(total, 256)), dim3(256), 0,
+                     s, a);
+  return check_hip(hipGetLastError(), "swa_trim launch");
+}
+
+}  // namespace mia

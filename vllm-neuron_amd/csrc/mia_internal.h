@@ -1,0 +1,47 @@
+// mia_internal.h — host-side declarations shared between the C-ABI layer
+// (abi.hip) and the kernel translation units.  Not part of the public ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "mia_attn.h"
+
+namespace mia {
+
+// Records `msg` as the calling thread's last error and returns `code`.
+int set_error(int code, const std::string &msg);
+
+// Checks a HIP call made while launching; converts failures to
+// MIA_ERR_RUNTIME with the HIP error string.
+int check_hip(hipError_t err, const char *what);
+
+// Kernel launchers (each defined next to its kernels).  They assume the
+// arguments were validated by the ABI layer.
+int launch_kv_write(const mia_kv_write_args &a, hipStream_t s);
+int launch_gather(const mia_gather_args &a, hipStream_t s);
+int launch_decode_mask(const mia_mask_args &a, hipStream_t s);
+int launch_slot_mapping(const mia_slot_mapping_args &a, hipStream_t s);
+int launch_remap_null(const int32_t *in, int32_t *out, int64_t n,
+                      int32_t null_block, hipStream_t s);
+int launch_swa_trim(const mia_swa_trim_args &a, hipStream_t s);
+int launch_packed_k(const mia_packed_k_args &a, hipStream_t s);
+int launch_scatter_rows(const mia_scatter_rows_args &a, hipStream_t s);
+
+// Paged decode: split-K plan shared by the workspace query and the launch.
+struct DecodePlan {
+  int split_tokens;  // tokens per split-K chunk
+  int num_splits;    // ceil(S_ctx / split_tokens)
+  int ncols;         // columns (query token x head of a GQA group) per launch
+  int col_groups;    // launches over column groups
+  size_t ws_bytes;   // workspace bytes
+};
+DecodePlan plan_decode(const mia_decode_args &a);
+int launch_paged_decode(const mia_decode_args &a, const DecodePlan &p,
+                        hipStream_t s);
+
+int launch_paged_prefill(const mia_prefill_args &a, hipStream_t s);
+
+}  // namespace mia

@@ -1,0 +1,709 @@
+// paged_decode.hip — split-K flash decoding over a block-table KV cache for
+// gfx950 (wave64, MFMA, 160 KB LDS).
+//
+// Work decomposition
+//   grid  = (num_splits, Hkv, B) per column group; 256 threads = 4 waves.
+//   A workgroup owns one (batch row b, kv head h, split) and every query
+//   column of that GQA group: column c = s * G + g (query token s, head
+//   g of the group), up to 16 columns per launch.  K/V bytes of a split are
+//   read from HBM exactly once and shared by all G*S_tkg queries.
+//   Each wave takes 64-token tiles of the split in turn.
+//
+// Per 64-token tile and wave
+//   K  : 4 sub-tiles of 16 tokens loaded straight into MFMA A-operand
+//        registers (lane = token row, 16 B = 8 consecutive d per lane; a
+//        load instruction covers 16 rows x 64 contiguous bytes).
+//   QK : v_mfma_f32_16x16x32_bf16, A = K [16 tok x 32 d], B = Q^T [32 d x
+//        16 columns]; D/32 k-steps.  Result lane l holds tokens
+//        4*(l/16)+i, column l%16.
+//   softmax: masked scores, tile max via xor-shuffles over 16/32 lanes,
+//        online rescale (exp2 domain), per-lane partial row sums.
+//   PV : on the vector ALU in fp32: lane = (token lane, 8-wide d slice),
+//        V rows loaded 16 B per lane (an instruction covers whole 256-byte
+//        rows), probabilities exchanged through LDS.
+//   Block-table lookups are wave-uniform (block_size % 16 == 0) and go
+//   through the scalar cache.
+// End of split: xor-reduce partial sums, merge the 4 waves through LDS and
+// write (m, l, o[D]) per column to the workspace.
+//
+// Combine kernel (grid = (Hkv, B)): merges the valid splits of a row, adds
+// the S_tkg active (new) keys — which the reference places at the last
+// S_tkg slots of the gathered context (attention_decode.py:957-982) — and
+// the optional sink logit (attention_decode.py:1019-1024), normalises and
+// writes bf16.
+#include <algorithm>
+
+#include "mia_device.h"
+#include "mia_internal.h"
+
+namespace mia {
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kTile = 64;  // tokens per wave tile
+constexpr int kPMax = 128;
+
+struct DecodeKParams {
+  const uint16_t *q;
+  int64_t qs_b, qs_s, qs_h;
+  const uint8_t *k_cache;
+  const uint8_t *v_cache;
+  int64_t kc_blk, kc_h, kc_t;  // element strides, d contiguous
+  int64_t vc_blk, vc_h, vc_t;
+  const int32_t *bt;
+  int64_t bt_b, bt_h, bt_j;
+  int bs;
+  int nb;  // physical blocks in the pool
+  FastDiv bs_div;
+  int B, S, Hq, Hkv, G, s_ctx;
+  int mask_mode;
+  const float *pos;
+  const float *start;
+  const float *full_mask;
+  int mask_bl;
+  float scale_log2;  // softmax_scale * log2(e) (* 256 for the fp8 decode)
+  const float *k_deq;
+  int split_tokens;
+  int num_splits;
+  int col0;    // first column of this launch
+  int nc_tot;  // G * S
+  float *ws_o;   // [B, Hkv, num_splits, nc_tot, D]
+  float *ws_ml;  // [B, Hkv, num_splits, nc_tot, 2]
+};
+
+struct RowInfo {
+  int lo, hi;     // prior slot range [lo, hi)
+  float minpos;   // min over the row's active tokens of pos_ids
+};
+
+// Prior-slot range of batch row b (shared by the split and combine kernels
+// so both agree on which splits hold data).
+MIA_DEV RowInfo row_info(const float *pos, const float *start, int mask_mode,
+                         int S, int s_ctx, int b) {
+  RowInfo r;
+  const int cap = s_ctx - S;
+  if (mask_mode == 1) {
+    r.lo = 0;
+    r.hi = cap;
+    r.minpos = 0.f;
+    return r;
+  }
+  float mp = pos[(int64_t)b * S];
+  for (int s = 1; s < S; ++s) mp = fminf(mp, pos[(int64_t)b * S + s]);
+  r.minpos = mp;
+  // integer j satisfies j < mp  <=>  j < ceil(mp)
+  float c = ceilf(mp);
+  int hi = c <= 0.f ? 0 : (c >= (float)cap ? cap : (int)c);
+  r.lo = 0;
+  r.hi = hi;
+  if (start) {
+    bool wrap = false;
+    float mst = 3.0e38f;
+    for (int s = 0; s < S; ++s) {
+      float st = start[(int64_t)b * S + s];
+      if (st > mp) wrap = true;
+      else mst = fminf(mst, st);
+    }
+    if (wrap) {
+      r.hi = cap;
+    } else {
+      float cs = ceilf(mst);
+      int lo = cs <= 0.f ? 0 : (cs >= (float)hi ? hi : (int)cs);
+      r.lo = lo;
+    }
+  }
+  if (r.hi < r.lo) r.hi = r.lo;
+  return r;
+}
+
+MIA_DEV int64_t seq_to_linear(int64_t pos, int bl) {
+  if (bl <= 0) return pos;
+  const int64_t fold = pos / ((int64_t)kPMax * bl);
+  const int64_t within = pos % ((int64_t)kPMax * bl);
+  const int64_t part = within / bl;
+  const int64_t off = within % bl;
+  return (fold * bl + off) * kPMax + part;
+}
+
+// 8 K elements of one token -> MFMA bf16 operand.
+template <bool FP8>
+struct KLoad;
+
+template <>
+struct KLoad<false> {
+  typedef u32x4_t raw_t;
+  static MIA_DEV raw_t load(const uint8_t *p) {
+    return *reinterpret_cast<const u32x4_t *>(p);
+  }
+  static MIA_DEV raw_t zero() { return raw_t{0u, 0u, 0u, 0u}; }
+  static MIA_DEV bf16x8_t to_bf16(raw_t r) {
+    return __builtin_bit_cast(bf16x8_t, r);
+  }
+};
+
+template <>
+struct KLoad<true> {
+  typedef u32x2_t raw_t;
+  static MIA_DEV raw_t load(const uint8_t *p) {
+    return *reinterpret_cast<const u32x2_t *>(p);
+  }
+  static MIA_DEV raw_t zero() { return raw_t{0u, 0u}; }
+  // values are x * 2^-8 (see e4m3fn_x4_to_f32_scaled); exact in bf16.
+  static MIA_DEV bf16x8_t to_bf16(raw_t r) {
+    float f[8];
+    e4m3fn_x4_to_f32_scaled(r[0], f);
+    e4m3fn_x4_to_f32_scaled(r[1], f + 4);
+    u32x4_t w;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      w[i] = (__float_as_uint(f[2 * i]) >> 16) |
+             (__float_as_uint(f[2 * i + 1]) & 0xffff0000u);
+    return __builtin_bit_cast(bf16x8_t, w);
+  }
+};
+
+template <bool FP8>
+MIA_DEV void v_to_f32(typename KLoad<FP8>::raw_t r, float v[8]);
+
+template <>
+MIA_DEV void v_to_f32<false>(u32x4_t r, float v[8]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    v[2 * i] = bf16lo(r[i]);
+    v[2 * i + 1] = bf16hi(r[i]);
+  }
+}
+
+template <>
+MIA_DEV void v_to_f32<true>(u32x2_t r, float v[8]) {
+  e4m3fn_x4_to_f32_scaled(r[0], v);
+  e4m3fn_x4_to_f32_scaled(r[1], v + 4);
+}
+
+// ---------------------------------------------------------------------------
+// split kernel
+// ---------------------------------------------------------------------------
+template <int D, int NCP, bool FP8>
+__global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeKParams p) {
+  constexpr int EB = FP8 ? 1 : 2;      // cache element bytes
+  constexpr int KSTEPS = D / 32;
+  constexpr int NSUB = kTile / 16;
+  constexpr int DS = D / 8;            // lanes per V row (8 elems each)
+  constexpr int TL = 64 / DS;          // V token lanes per wave
+  constexpr int VPL = kTile / TL;      // V tokens per lane per tile
+  using KL = KLoad<FP8>;
+  using raw_t = typename KL::raw_t;
+
+  __shared__ float p_lds[kWaves][kTile][NCP];
+  __shared__ float a_lds[kWaves][16];
+  __shared__ float red_lds[kWaves][NCP][D + 2];
+
+  const int split = blockIdx.x;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+
+  const RowInfo ri = row_info(p.pos, p.start, p.mask_mode, p.S, p.s_ctx, b);
+  const int c_lo = max(ri.lo, split * p.split_tokens);
+  const int c_hi = min(ri.hi, (split + 1) * p.split_tokens);
+  if (c_lo >= c_hi) return;  // uniform over the workgroup
+
+  // ---- query column owned by this lane in the QK layout
+  const int qcol = lane & 15;
+  const int kg = lane >> 4;  // k-group (8 d-values) / token quad
+  const int gcol = p.col0 + qcol;
+  const bool col_ok = (qcol < NCP) && (gcol < p.nc_tot);
+  const int s_q = col_ok ? gcol / p.G : 0;
+  const int hq = h * p.G + (col_ok ? gcol % p.G : 0);
+  float st_q = 0.f;
+  bool wrap_q = false;
+  if (p.mask_mode == 0 && p.start && col_ok) {
+    st_q = p.start[(int64_t)b * p.S + s_q];
+    wrap_q = st_q > ri.minpos;
+  }
+
+  bf16x8_t qf[KSTEPS];
+  {
+    const uint16_t *qp = p.q + b * p.qs_b + (int64_t)s_q * p.qs_s + hq * p.qs_h;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      u32x4_t w = {0u, 0u, 0u, 0u};
+      if (col_ok)
+        w = *reinterpret_cast<const u32x4_t *>(qp + ks * 32 + kg * 8);
+      qf[ks] = __builtin_bit_cast(bf16x8_t, w);
+    }
+  }
+
+  const float scale2 = p.scale_log2 * (p.k_deq ? p.k_deq[h] : 1.0f);
+  const int64_t bt_row = (int64_t)b * p.bt_b + (int64_t)h * p.bt_h;
+
+  // PV lane roles
+  const int ds = lane % DS;
+  const int tl = lane / DS;
+
+  float m_run = -INFINITY;  // per column (lane & 15)
+  float l_run = 0.f;        // per lane partial
+  float o[NCP][8];
+#pragma unroll
+  for (int c = 0; c < NCP; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[c][e] = 0.f;
+
+  const int chunk0 = split * p.split_tokens;
+  for (int t0 = chunk0 + wave * kTile; t0 < c_hi; t0 += kWaves * kTile) {
+    if (t0 + kTile <= c_lo) continue;  // uniform
+
+    // ---- K loads (A operand), 4 sub-tiles of 16 tokens
+    raw_t kr[NSUB][KSTEPS];
+#pragma unroll
+    for (int st = 0; st < NSUB; ++st) {
+      const int tb = t0 + st * 16;  // uniform, multiple of 16
+      const int tok = tb + qcol;
+      const bool ok = tok >= c_lo && tok < c_hi;
+      const uint32_t blk_i = fdiv((uint32_t)tb, p.bs_div);
+      int32_t phys = 0;
+      if (tb < c_hi) phys = p.bt[bt_row + (int64_t)blk_i * p.bt_j];
+      phys = phys < 0 ? 0 : (phys >= p.nb ? p.nb - 1 : phys);
+      const int in_blk = tb - (int)blk_i * p.bs + qcol;
+      const uint8_t *kp = p.k_cache +
+          ((int64_t)phys * p.kc_blk + (int64_t)h * p.kc_h +
+           (int64_t)in_blk * p.kc_t) * EB;
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        kr[st][ks] = ok ? KL::load(kp + (ks * 32 + kg * 8) * EB) : KL::zero();
+      }
+    }
+    // ---- V loads (VALU layout)
+    raw_t vr[VPL];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      const int tb = t0 + i * TL;  // uniform
+      const int tok = tb + tl;
+      const bool ok = tok >= c_lo && tok < c_hi;
+      const uint32_t blk_i = fdiv((uint32_t)tb, p.bs_div);
+      int32_t phys = 0;
+      if (tb < c_hi) phys = p.bt[bt_row + (int64_t)blk_i * p.bt_j];
+      phys = phys < 0 ? 0 : (phys >= p.nb ? p.nb - 1 : phys);
+      const int in_blk = tb - (int)blk_i * p.bs + tl;
+      const uint8_t *vp = p.v_cache +
+          ((int64_t)phys * p.vc_blk + (int64_t)h * p.vc_h +
+           (int64_t)in_blk * p.vc_t + ds * 8) * EB;
+      vr[i] = ok ? KL::load(vp) : KL::zero();
+    }
+
+    // ---- QK^T on MFMA
+    float sc[NSUB][4];
+#pragma unroll
+    for (int st = 0; st < NSUB; ++st) {
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(KL::to_bf16(kr[st][ks]),
+                                                      qf[ks], acc, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int tok = t0 + st * 16 + kg * 4 + i;
+        bool ok = col_ok && tok >= c_lo && tok < c_hi;
+        if (ok) {
+          if (p.mask_mode == 1) {
+            const int64_t lin = seq_to_linear(tok, p.mask_bl);
+            const int64_t mi = ((lin * p.B + b) * p.Hq + hq) * p.S + s_q;
+            ok = p.full_mask[mi] != 0.f;
+          } else if (p.start) {
+            const float ft = (float)tok;
+            ok = wrap_q ? (ft >= st_q || ft < ri.minpos)
+                        : (ft >= st_q && ft < ri.minpos);
+          }
+        }
+        sc[st][i] = ok ? acc[i] * scale2 : -INFINITY;
+      }
+    }
+
+    // ---- online softmax (exp2 domain)
+    float mx = -INFINITY;
+#pragma unroll
+    for (int st = 0; st < NSUB; ++st)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[st][i]);
+    mx = wave_max_xor(mx, 16);
+    mx = wave_max_xor(mx, 32);
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    m_run = m_new;
+    float psum = 0.f;
+#pragma unroll
+    for (int st = 0; st < NSUB; ++st) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pv = __builtin_amdgcn_exp2f(sc[st][i] - m_use);
+        psum += pv;
+        if (qcol < NCP) p_lds[wave][st * 16 + kg * 4 + i][qcol] = pv;
+      }
+    }
+    l_run = l_run * alpha + psum;
+    if (lane < 16) a_lds[wave][lane] = alpha;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+
+    // ---- PV on the vector ALU
+    float al[NCP];
+#pragma unroll
+    for (int c = 0; c < NCP; ++c) al[c] = a_lds[wave][c];
+#pragma unroll
+    for (int c = 0; c < NCP; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[c][e] *= al[c];
+#pragma unroll
+    for (int i = 0; i < VPL; ++i) {
+      float v[8];
+      v_to_f32<FP8>(vr[i], v);
+      const int tloc = i * TL + tl;
+      float pc[NCP];
+#pragma unroll
+      for (int c = 0; c < NCP; ++c) pc[c] = p_lds[wave][tloc][c];
+#pragma unroll
+      for (int c = 0; c < NCP; ++c)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[c][e] = fmaf(pc[c], v[e], o[c][e]);
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  }
+
+  // ---- reduce within the wave
+  l_run = wave_sum_xor(l_run, 16);
+  l_run = wave_sum_xor(l_run, 32);
+#pragma unroll
+  for (int c = 0; c < NCP; ++c)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float x = o[c][e];
+#pragma unroll
+      for (int msk = DS; msk < 64; msk <<= 1) x = wave_sum_xor(x, msk);
+      o[c][e] = x;
+    }
+
+  // ---- merge the waves through LDS
+  if (lane < NCP) {
+    red_lds[wave][lane][D] = m_run;
+    red_lds[wave][lane][D + 1] = l_run;
+  }
+  if (tl == 0) {
+#pragma unroll
+    for (int c = 0; c < NCP; ++c)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) red_lds[wave][c][ds * 8 + e] = o[c][e];
+  }
+  __syncthreads();
+
+  const int64_t ws_row =
+      (((int64_t)b * p.Hkv + h) * p.num_splits + split) * p.nc_tot;
+  for (int idx = threadIdx.x; idx < NCP * D; idx += blockDim.x) {
+    const int c = idx / D;
+    const int d = idx % D;
+    const int gc = p.col0 + c;
+    if (gc >= p.nc_tot) continue;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, red_lds[w][c][D]);
+    const float Mu = (M == -INFINITY) ? 0.f : M;
+    float acc = 0.f, L = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float wt = __builtin_amdgcn_exp2f(red_lds[w][c][D] - Mu);
+      acc += red_lds[w][c][d] * wt;
+      L += red_lds[w][c][D + 1] * wt;
+    }
+    p.ws_o[(ws_row + gc) * D + d] = acc;
+    if (d == 0) {
+      p.ws_ml[(ws_row + gc) * 2] = M;
+      p.ws_ml[(ws_row + gc) * 2 + 1] = L;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// combine kernel
+// ---------------------------------------------------------------------------
+struct CombineParams {
+  DecodeKParams k;  // shared geometry (col0 unused)
+  int D;
+  const uint16_t *k_new;
+  const uint16_t *v_new;
+  int64_t kn_b, kn_s, kn_h;
+  int64_t vn_b, vn_s, vn_h;
+  const float *active_mask;  // [S, B, Hq, S] or null
+  const float *sink;         // [Hq] or null
+  const float *v_deq;
+  float act_scale_log2;      // softmax_scale * log2(e)
+  int fp8;                   // round-trip active rows through e4m3fn
+  int quant_mode;
+  const float *k_quant;
+  const float *v_quant;
+  int quant_per_head;
+  uint16_t *out;
+  int64_t os_b, os_s, os_h;
+};
+
+constexpr int kMaxCols = 64;
+constexpr int kMaxAct = 16;
+
+MIA_DEV float active_value(const CombineParams &c, const uint16_t *base,
+                           int64_t idx, int h, const float *qscale) {
+  float x = bf16_bits_to_f32(base[idx]);
+  if (c.quant_mode == MIA_QUANT_NONE) return x;
+  const float s = qscale[c.quant_per_head ? h : 0];
+  return e4m3fn_bits_to_f32(quantize_e4m3fn(x, s, c.quant_mode));
+}
+
+__global__ __launch_bounds__(256) void decode_combine_kernel(CombineParams c) {
+  const DecodeKParams &p = c.k;
+  const int h = blockIdx.x;
+  const int b = blockIdx.y;
+  const int D = c.D;
+  const int NC = p.nc_tot;
+  const int S = p.S;
+  const int wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+
+  __shared__ float act[kMaxCols][kMaxAct];
+  __shared__ float colM[kMaxCols];
+  __shared__ float colL[kMaxCols];
+
+  const RowInfo ri = row_info(p.pos, p.start, p.mask_mode, S, p.s_ctx, b);
+  int sp0 = 0, sp1 = 0;
+  if (ri.lo < ri.hi) {
+    sp0 = ri.lo / p.split_tokens;
+    sp1 = (ri.hi + p.split_tokens - 1) / p.split_tokens;
+  }
+  const float kdeq = p.k_deq ? p.k_deq[h] : 1.0f;
+  const float ascale = c.act_scale_log2 * kdeq;
+  const int64_t row0 = ((int64_t)b * p.Hkv + h) * p.num_splits;
+
+  // 1) active-token scores: one wave per (column, key) pair, lanes over d.
+  for (int pair = wave; pair < NC * S; pair += kWaves) {
+    const int col = pair / S;
+    const int k = pair % S;
+    const int s_q = col / p.G;
+    const int hq = h * p.G + col % p.G;
+    bool ok;
+    if (p.mask_mode == 1) {
+      const int64_t lin = seq_to_linear((int64_t)p.s_ctx - S + k, p.mask_bl);
+      ok = p.full_mask[((lin * p.B + b) * p.Hq + hq) * S + s_q] != 0.f;
+    } else if (c.active_mask) {
+      ok = c.active_mask[(((int64_t)k * p.B + b) * p.Hq + hq) * S + s_q] != 0.f;
+    } else {
+      ok = k <= s_q;
+    }
+    const uint16_t *qp = p.q + b * p.qs_b + (int64_t)s_q * p.qs_s + hq * p.qs_h;
+    const int64_t kb = b * c.kn_b + (int64_t)k * c.kn_s + (int64_t)h * c.kn_h;
+    float dot = 0.f;
+    for (int d = lane; d < D; d += 64)
+      dot = fmaf(bf16_bits_to_f32(qp[d]),
+                 active_value(c, c.k_new, kb + d, h, c.k_quant), dot);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) dot = wave_sum_xor(dot, m);
+    if (lane == 0) act[col][k] = ok ? dot * ascale : -INFINITY;
+  }
+  __syncthreads();
+
+  // 2) per-column max and denominator: one wave per column, lanes over splits.
+  for (int col = wave; col < NC; col += kWaves) {
+    const int hq = h * p.G + col % p.G;
+    const float sink2 = c.sink ? c.sink[hq] * kLog2e : -INFINITY;
+    float M = -INFINITY;
+    for (int sp = sp0 + lane; sp < sp1; sp += 64)
+      M = fmaxf(M, p.ws_ml[((row0 + sp) * NC + col) * 2]);
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) M = wave_max_xor(M, m);
+    M = fmaxf(M, sink2);
+    for (int k = 0; k < S; ++k) M = fmaxf(M, act[col][k]);
+    const float Mu = (M == -INFINITY) ? 0.f : M;
+    float L = 0.f;
+    for (int sp = sp0 + lane; sp < sp1; sp += 64) {
+      const int64_t r = (row0 + sp) * NC + col;
+      L += p.ws_ml[r * 2 + 1] * __builtin_amdgcn_exp2f(p.ws_ml[r * 2] - Mu);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) L = wave_sum_xor(L, m);
+    if (lane == 0) {
+      L += __builtin_amdgcn_exp2f(sink2 - Mu);
+      for (int k = 0; k < S; ++k) L += __builtin_amdgcn_exp2f(act[col][k] - Mu);
+      colM[col] = Mu;
+      colL[col] = L;
+    }
+  }
+  __syncthreads();
+
+  // 3) output: one thread per (column, d); split loads are independent and
+  // unrolled so they are in flight together.
+  const float vdeq = (c.v_deq ? c.v_deq[h] : 1.0f);
+  const float vpart_scale = c.fp8 ? 256.0f : 1.0f;  // fp8 partials hold v*2^-8
+  for (int idx = threadIdx.x; idx < NC * D; idx += blockDim.x) {
+    const int col = idx / D;
+    const int d = idx % D;
+    const int s_q = col / p.G;
+    const int hq = h * p.G + col % p.G;
+    const float Mu = colM[col];
+    float acc = 0.f;
+#pragma unroll 8
+    for (int sp = sp0; sp < sp1; ++sp) {
+      const int64_t r = (row0 + sp) * NC + col;
+      acc += p.ws_o[r * D + d] * __builtin_amdgcn_exp2f(p.ws_ml[r * 2] - Mu);
+    }
+    acc *= vpart_scale;
+    for (int k = 0; k < S; ++k) {
+      const float pk = __builtin_amdgcn_exp2f(act[col][k] - Mu);
+      if (pk != 0.f) {
+        const int64_t vb = b * c.vn_b + (int64_t)k * c.vn_s + (int64_t)h * c.vn_h;
+        acc += pk * active_value(c, c.v_new, vb + d, h, c.v_quant);
+      }
+    }
+    const float outv = acc / colL[col] * vdeq;
+    c.out[b * c.os_b + (int64_t)s_q * c.os_s + hq * c.os_h + d] =
+        (uint16_t)f32_to_bf16_bits(outv);
+  }
+}
+
+template <int D, int NCP, bool FP8>
+void launch_split(const DecodeKParams &kp, dim3 grid, hipStream_t s) {
+  hipLaunchKernelGGL((decode_split_kernel<D, NCP, FP8>), grid, dim3(256), 0, s,
+                     kp);
+}
+
+template <int D, bool FP8>
+void launch_split_ncp(int ncp, const DecodeKParams &kp, dim3 grid,
+                      hipStream_t s) {
+  if (ncp <= 4) launch_split<D, 4, FP8>(kp, grid, s);
+  else if (ncp <= 8) launch_split<D, 8, FP8>(kp, grid, s);
+  else launch_split<D, 16, FP8>(kp, grid, s);
+}
+
+}  // namespace
+
+DecodePlan plan_decode(const mia_decode_args &a) {
+  DecodePlan pl;
+  const int G = a.num_q_heads / a.num_kv_heads;
+  const int s_ctx = a.blocks_per_seq * a.block_size;
+  int st = a.split_tokens;
+  if (st <= 0) {
+    // Shape-only choice (graph-capturable, no host sync): aim for ~8k
+    // workgroups over the worst case B*Hkv*S_ctx, chunks of 256..4096
+    // tokens in powers of two.
+    const int64_t work = (int64_t)a.batch * a.num_kv_heads * s_ctx;
+    int64_t want = work / 8192;
+    st = 256;
+    while (st < want && st < 4096) st <<= 1;
+  }
+  st = ((st + kWaves * kTile - 1) / (kWaves * kTile)) * (kWaves * kTile);
+  pl.split_tokens = st;
+  pl.num_splits = s_ctx > 0 ? (s_ctx + st - 1) / st : 0;
+  if (pl.num_splits < 1) pl.num_splits = 1;
+  pl.ncols = G * a.s_active;
+  pl.col_groups = (pl.ncols + 15) / 16;
+  const size_t rows = (size_t)a.batch * a.num_kv_heads * pl.num_splits * pl.ncols;
+  size_t o_bytes = rows * (size_t)a.head_dim * sizeof(float);
+  o_bytes = (o_bytes + 255) & ~(size_t)255;
+  pl.ws_bytes = o_bytes + rows * 2 * sizeof(float);
+  return pl;
+}
+
+int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
+                        hipStream_t s) {
+  const int G = a.num_q_heads / a.num_kv_heads;
+  const bool fp8 = a.cache_dtype == MIA_DTYPE_FP8_E4M3FN;
+  DecodeKParams kp;
+  kp.q = (const uint16_t *)a.q;
+  kp.qs_b = a.q_stride[0];
+  kp.qs_s = a.q_stride[1];
+  kp.qs_h = a.q_stride[2];
+  kp.k_cache = (const uint8_t *)a.k_cache;
+  kp.v_cache = (const uint8_t *)a.v_cache;
+  kp.kc_blk = a.k_cache_stride[0];
+  kp.kc_h = a.k_cache_stride[1];
+  kp.kc_t = a.k_cache_stride[2];
+  kp.vc_blk = a.v_cache_stride[0];
+  kp.vc_h = a.v_cache_stride[1];
+  kp.vc_t = a.v_cache_stride[2];
+  kp.bt = a.block_table;
+  kp.bt_b = a.bt_stride[0];
+  kp.bt_h = a.bt_stride[1];
+  kp.bt_j = a.bt_stride[2];
+  kp.bs = a.block_size;
+  kp.nb = a.num_blocks;
+  kp.bs_div = make_fastdiv((uint32_t)a.block_size);
+  kp.B = a.batch;
+  kp.S = a.s_active;
+  kp.Hq = a.num_q_heads;
+  kp.Hkv = a.num_kv_heads;
+  kp.G = G;
+  kp.s_ctx = a.blocks_per_seq * a.block_size;
+  kp.mask_mode = a.mask_mode;
+  kp.pos = a.pos_ids;
+  kp.start = a.start_pos;
+  kp.full_mask = a.full_mask;
+  kp.mask_bl = a.mask_block_len;
+  kp.scale_log2 = a.softmax_scale * kLog2e * (fp8 ? 256.0f : 1.0f);
+  kp.k_deq = a.k_dequant;
+  kp.split_tokens = pl.split_tokens;
+  kp.num_splits = pl.num_splits;
+  kp.nc_tot = pl.ncols;
+  const size_t rows = (size_t)a.batch * a.num_kv_heads * pl.num_splits * pl.ncols;
+  size_t o_bytes = rows * (size_t)a.head_dim * sizeof(float);
+  o_bytes = (o_bytes + 255) & ~(size_t)255;
+  kp.ws_o = (float *)a.workspace;
+  kp.ws_ml = (float *)((char *)a.workspace + o_bytes);
+
+  const dim3 grid((unsigned)pl.num_splits, (unsigned)a.num_kv_heads,
+                  (unsigned)a.batch);
+  if (pl.num_splits > 0 && kp.s_ctx - kp.S > 0) {
+    for (int cg = 0; cg < pl.col_groups; ++cg) {
+      kp.col0 = cg * 16;
+      const int ncp = std::min(16, pl.ncols - kp.col0);
+      if (a.head_dim == 128) {
+        if (fp8) launch_split_ncp<128, true>(ncp, kp, grid, s);
+        else launch_split_ncp<128, false>(ncp, kp, grid, s);
+      } else {
+        if (fp8) launch_split_ncp<64, true>(ncp, kp, grid, s);
+        else launch_split_ncp<64, false>(ncp, kp, grid, s);
+      }
+      int rc = check_hip(hipGetLastError(), "decode split launch");
+      if (rc) return rc;
+    }
+  }
+  kp.col0 = 0;
+  CombineParams cp;
+  cp.k = kp;
+  cp.D = a.head_dim;
+  cp.k_new = (const uint16_t *)a.k_new;
+  cp.v_new = (const uint16_t *)a.v_new;
+  cp.kn_b = a.k_new_stride[0];
+  cp.kn_s = a.k_new_stride[1];
+  cp.kn_h = a.k_new_stride[2];
+  cp.vn_b = a.v_new_stride[0];
+  cp.vn_s = a.v_new_stride[1];
+  cp.vn_h = a.v_new_stride[2];
+  cp.active_mask = a.active_mask;
+  cp.sink = a.sink;
+  cp.v_deq = a.v_dequant;
+  cp.act_scale_log2 = a.softmax_scale * kLog2e;
+  cp.fp8 = fp8 ? 1 : 0;
+  cp.quant_mode = a.quant_mode;
+  cp.k_quant = a.k_quant;
+  cp.v_quant = a.v_quant;
+  cp.quant_per_head = a.quant_per_head;
+  cp.out = (uint16_t *)a.out;
+  cp.os_b = a.out_stride[0];
+  cp.os_s = a.out_stride[1];
+  cp.os_h = a.out_stride[2];
+  hipLaunchKernelGGL(decode_combine_kernel,
+                     dim3((unsigned)a.num_kv_heads, (unsigned)a.batch),
+                     dim3(256), 0, s, cp);
+  return check_hip(hipGetLastError(), "decode combine launch");
+}
+
+}  // namespace mia
