@@ -1,0 +1,253 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X paged-KV attention path; prints ONE JSON line.
+
+Workload (N=1): Llama-3-8B-shaped paged decode — 32 q / 8 kv heads,
+head_dim 128, bf16, batch 64, contexts U[512, 8192], block_size 32, random
+non-contiguous block tables, N(0,1) inputs.  A step is one decode attention
+pass over the batch: the split-K attention kernels plus the KV-cache write
+of the 64 new tokens, inputs resident in HBM.
+
+The same line carries
+  * ``roofline`` for the dominant kernel (the split-K decode kernel, HBM
+    bound), timed with HIP events recorded on its own stream;
+  * ``prefill``: the chunked-prefill sub-batch of the mixed Llama-3-8B
+    workload (4 sequences x 512 new tokens on priors U[0, 4096]) in TFLOP/s
+    against the bf16 MFMA peak;
+  * ``cpu_baseline``: the CPU restatement of the reference's torch decode
+    path on a bounded sample of the same workload, timed on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT, ROOT / "vllm-neuron_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
+BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, TFLOP/s
+METRIC = "decode-attn KV GB/s (% of HBM peak) + prefill TFLOP/s at 8B shape, 1 GPU"
+
+
+def _decode_step_fn(b, dev):
+    import torch
+
+    from vllm_neuron_amd import _kernels as K
+    from vllm_neuron_amd.functional.attention.attention_decode import paged_decode_core
+
+    cfg = b.cfg
+    S_ctx = b.block_table.shape[1] * cfg.block_size
+    out = torch.empty_like(b.q)
+    # workspace sized once (the library never allocates)
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    k_rows = b.k_new.reshape(cfg.batch, cfg.kv_heads, cfg.head_dim)
+    v_rows = b.v_new.reshape(cfg.batch, cfg.kv_heads, cfg.head_dim)
+
+    def step(events=None):
+        paged_decode_core(b.q, b.k_new, b.v_new, b.k_cache, b.v_cache, b.block_table,
+                          block_len=cfg.block_size, S_ctx=S_ctx, pos_ids=b.pos,
+                          softmax_scale=cfg.head_dim ** -0.5, workspace=ws,
+                          split_events=events)
+        K.kv_write(k_rows, v_rows, b.slots, b.k_cache, b.v_cache)
+        return out
+
+    return step
+
+
+def bench_decode(dev, steps, warmup):
+    import torch
+
+    from vllm_neuron_amd import workloads as W
+
+    cfg = W.DECODE_CONFIGS["llama3_8b_decode_b64"]
+    b = W.make_decode_batch(cfg, dev)
+    step = _decode_step_fn(b, dev)
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    for e0, e1 in ev:  # create the HIP events on this device/stream
+        e0.record()
+        e1.record()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        step(ev[i])
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    ms_step = (t1 - t0) * 1e3 / steps
+    split_ms = [e0.elapsed_time(e1) for e0, e1 in ev]
+    total_bytes = W.decode_bytes(b)
+    # algorithmic bytes of one split-K launch: prior K/V rows attended
+    # (the new token is merged by the combine kernel), Q, and the block
+    # table entries of the attended blocks
+    L = (b.ctx.cpu().to(torch.int64) - 1)
+    split_bytes = (int(L.sum()) * cfg.kv_heads * cfg.head_dim * 2 * 2
+                   + cfg.batch * cfg.q_heads * cfg.head_dim * 2
+                   + int(((L + cfg.block_size - 1) // cfg.block_size).sum()) * 4)
+    split_avg_ms = statistics.mean(split_ms)
+    return dict(cfg=cfg, batch=b, ms_step=ms_step, total_bytes=total_bytes,
+                split_bytes=split_bytes, split_avg_ms=split_avg_ms,
+                split_med_ms=statistics.median(split_ms))
+
+
+def bench_prefill(dev, steps, warmup):
+    import torch
+
+    from vllm_neuron_amd import _kernels as K
+    from vllm_neuron_amd import workloads as W
+
+    cfg = W.PREFILL_CONFIGS["llama3_8b_prefill_4x512"]
+    b = W.make_prefill_batch(cfg, dev)
+    K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache)
+    out = torch.empty_like(b.q)
+
+    def step():
+        K.paged_prefill(b.q, b.cu_seqlens, b.prior, b.max_seqlen_q, b.k_cache, b.v_cache,
+                        b.block_table, scale=cfg.head_dim ** -0.5, out=out)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    times = []
+    for _ in range(steps):
+        e0.record()
+        step()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+    flops = W.prefill_flops(b)
+    ms = statistics.mean(times)
+    return dict(flops=flops, ms=ms, ms_med=statistics.median(times),
+                tflops=flops / (ms * 1e-3) / 1e12)
+
+
+def cpu_baseline(gpu_batch, rows=16):
+    """The oracle (CPU restatement of the reference torch decode path,
+    attention_decode.py:653-1182, mask pre-generated as the Llama caller
+    does) on the first ``rows`` batch rows of the same Llama-3-8B decode
+    batch, copied to host memory.  Returns GB/s of the algorithmic bytes
+    of the sampled rows (same formula as the GPU line)."""
+    import torch
+
+    from oracle import decode as OD
+    from oracle import mask as OM
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", 0)) or (os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    cfg = gpu_batch.cfg
+    B, Hq, Hkv, d, bs = cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.block_size
+    rows = min(rows, B)
+    kc, vc = gpu_batch.k_cache.cpu(), gpu_batch.v_cache.cpu()
+    q, kn, vn = (t[:rows].cpu() for t in (gpu_batch.q, gpu_batch.k_new, gpu_batch.v_new))
+    table = gpu_batch.block_table[:rows].cpu()
+    pos = gpu_batch.pos[:rows].cpu()
+    S_ctx = table.shape[1] * bs
+    X = torch.cat([q.reshape(rows, 1, -1), kn.reshape(rows, 1, -1), vn.reshape(rows, 1, -1)], -1)
+    Wq = torch.eye(X.shape[-1], dtype=torch.bfloat16)
+    mask = OM.gen_mask_torch(pos.reshape(1, -1), rows, Hq, 1, S_ctx, block_len=bs)
+    times = []
+    for _ in range(4):  # 1 warm-up + median of 3
+        t0 = time.perf_counter()
+        OD.ref_attention_decode(X, Wq, kc, vc, table, mask)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times[1:])
+    L = gpu_batch.ctx[:rows].cpu().to(torch.int64)
+    nbytes = (int(L.sum()) * Hkv * d * 2 * 2 + rows * Hq * d * 2 * 2
+              + rows * Hkv * d * 2 * 2 + int(((L + bs - 1) // bs).sum()) * 4)
+    return {
+        "value": round(nbytes / t / 1e9, 4),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"first {rows} of {B} batch rows of the Llama-3-8B decode batch; "
+                   f"{t * 1e3:.1f} ms per call, median of 3 after 1 warm-up; "
+                   "restated reference torch decode path (bf16, pre-generated mask)"),
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-rows", type=int, default=16,
+                    help="batch rows of the decode batch timed on the CPU")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
+              "(the attention path is single-GPU in this build)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    dev = torch.device("cuda:0")
+    from vllm_neuron_amd import _native
+
+    _native.lib()
+    dec = bench_decode(dev, args.steps, args.warmup)
+    pre = bench_prefill(dev, max(5, args.steps // 2), max(2, args.warmup // 2))
+    cfg = dec["cfg"]
+    value = dec["total_bytes"] / (dec["ms_step"] * 1e-3) / 1e9
+    achieved = dec["split_bytes"] / (dec["split_avg_ms"] * 1e-3) / 1e9
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dec["ms_step"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) Q/K/V and cache, random block tables)",
+        "config": {
+            "workload": "llama3_8b_paged_decode_b64_ctx512-8192",
+            "batch": cfg.batch, "q_heads": cfg.q_heads, "kv_heads": cfg.kv_heads,
+            "head_dim": cfg.head_dim, "block_size": cfg.block_size,
+            "ctx_range": [cfg.ctx_lo, cfg.ctx_hi],
+            "kv_bytes_per_step": dec["total_bytes"],
+            "hbm_frac_of_step": round(value / HBM_PEAK_GBS, 4),
+        },
+        "roofline": {
+            "kernel": "decode_split_kernel<128,4,bf16>",
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "avg_launch_us": round(dec["split_avg_ms"] * 1e3, 2),
+            "algorithmic_bytes": dec["split_bytes"],
+        },
+        "prefill": {
+            "workload": "llama3_8b_chunked_prefill_4x512_prior0-4096",
+            "us_per_call": round(pre["ms"] * 1e3, 2),
+            "tflops": round(pre["tflops"], 2),
+            "peak_tflops": BF16_PEAK_TFLOPS,
+            "frac": round(pre["tflops"] / BF16_PEAK_TFLOPS, 4),
+            "flops": pre["flops"],
+        },
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(dec["batch"], args.cpu_rows)
+    else:
+        line["cpu_baseline"] = None
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -239,6 +239,11 @@ typedef struct {
   size_t workspace_bytes;
   int32_t split_tokens; /* tokens per split-K chunk; 0 = default */
   int32_t _pad1;
+  /* Optional timing instrumentation: hipEvent_t handles recorded on the
+   * stream right before the first and right after the last split-K launch
+   * (the combine kernel is outside).  NULL = not recorded. */
+  void *split_event_begin;
+  void *split_event_end;
 } mia_decode_args;
 
 size_t mia_decode_workspace_bytes(const mia_decode_args *args);

@@ -192,7 +192,7 @@ def test_full_mask_mode_matches_positions(gpu):
     content it must give the positions path's result."""
     # even batch: the reference's mask order is defined (odd batches with
     # s_prior % 256 != 0 raise IndexError there)
-    cfg = _small_cfg(batch=4, q_heads=16, kv_heads=2, head_dim=64, block_size=32,
+    cfg = _small_cfg(batch=4, q_heads=32, kv_heads=4, head_dim=64, block_size=32,
                      ctx_lo=100, ctx_hi=600)
     b = _make(cfg, gpu)
     B, Hq = cfg.batch, cfg.q_heads

@@ -1,0 +1,159 @@
+"""GPU parity of chunked (segmented) prefill and of the mixed batch against
+the CPU oracle (restated reference segmented path and float64 math)."""
+import pytest
+import torch
+
+from oracle import decode as OD
+from oracle import segmented as OSg
+from vllm_neuron_amd import _kernels as K
+from vllm_neuron_amd import workloads as W
+from vllm_neuron_amd.functional import mixed_batch_attention, segmented_attention
+
+pytestmark = pytest.mark.gpu
+
+TOL_BF16 = 2e-2
+TOL_FP8 = 6e-2
+
+
+def _seq_kv(cache, table_row, n, H):
+    return torch.stack([OD.gather_contiguous(cache, table_row, n, h) for h in range(H)])
+
+
+PREFILL_CASES = [
+    # q_heads, kv_heads, d, bs, new, prior, window, sink, tp_q, tp_out
+    (8, 2, 128, 32, 96, 64, 0, False, True, False),
+    (8, 2, 64, 16, 130, 0, 0, False, True, True),
+    (12, 2, 128, 64, 200, 128, 0, True, False, False),
+    (16, 2, 64, 32, 160, 96, 64, True, True, True),
+    (4, 4, 128, 16, 33, 48, 0, False, True, False),
+    (8, 1, 64, 32, 257, 512, 128, False, True, False),
+]
+
+
+@pytest.mark.parametrize("case", range(len(PREFILL_CASES)))
+def test_segmented_vs_reference(gpu, case):
+    Hq, Hkv, d, bs, S, prior, win, use_sink, tp_q, tp_out = PREFILL_CASES[case]
+    cfg = W.PrefillConfig("t", 1, Hq, Hkv, d, bs, S, prior, prior, seed=50 + case)
+    b = W.make_prefill_batch(cfg, gpu)
+    K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache)
+    q = b.q.transpose(0, 1).contiguous()  # [Nh, S, D]
+    if not tp_q:
+        q = q.transpose(1, 2).contiguous()
+    sink = torch.randn(Hq, generator=torch.Generator().manual_seed(case)).to(gpu) if use_sink else None
+    scale = d ** -0.5
+    out = segmented_attention(q, b.k_cache, b.v_cache, b.block_table, b.prior.view(1, 1), bs, 0,
+                              scale=scale, tp_q=tp_q, tp_out=tp_out, sliding_window=win or None,
+                              sink=None if sink is None else sink.view(Hq, 1))
+    ref = OSg.ref_segmented_attention(q.cpu(), b.k_cache.cpu(), b.v_cache.cpu(),
+                                      b.block_table.cpu(), b.prior.cpu().view(1, 1), bs, scale,
+                                      tp_q=tp_q, tp_out=tp_out, sliding_window=win or None,
+                                      sink=None if sink is None else sink.cpu().view(Hq, 1))
+    assert out.shape == ref.shape
+    err = (out.float().cpu() - ref.float()).abs().max().item()
+    assert err <= TOL_BF16, err
+    # float64 math on the contiguous sequence
+    n = prior + S
+    ks = _seq_kv(b.k_cache.cpu(), b.block_table[0].cpu(), n, Hkv)
+    vs = _seq_kv(b.v_cache.cpu(), b.block_table[0].cpu(), n, Hkv)
+    f = OSg.fp32_prefill(b.q.cpu(), ks, vs, prior, scale, win, None if sink is None else sink.cpu())
+    o = out.float().cpu()
+    o = o.transpose(1, 2) if tp_out else o
+    err64 = (o.transpose(0, 1).double() - f).abs().max().item()
+    assert err64 <= TOL_BF16, err64
+
+
+def test_varlen_matches_per_sequence(gpu):
+    """The 4 x 512 chunked-prefill sub-batch (priors U[0, 4096]) in one
+    varlen launch equals one segmented_attention call per sequence."""
+    cfg = W.PREFILL_CONFIGS["llama3_8b_prefill_4x512"]
+    b = W.make_prefill_batch(cfg, gpu)
+    K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache)
+    out = K.paged_prefill(b.q, b.cu_seqlens, b.prior, b.max_seqlen_q, b.k_cache, b.v_cache,
+                          b.block_table, scale=cfg.head_dim ** -0.5)
+    for i in range(cfg.num_seqs):
+        s0, s1 = int(b.cu_seqlens[i]), int(b.cu_seqlens[i + 1])
+        q = b.q[s0:s1].transpose(0, 1).contiguous()
+        ref = OSg.ref_segmented_attention(q.cpu(), b.k_cache.cpu(), b.v_cache.cpu(),
+                                          b.block_table[i:i + 1].cpu(), b.prior[i:i + 1].cpu(),
+                                          cfg.block_size, cfg.head_dim ** -0.5)
+        err = (out[s0:s1].transpose(0, 1).float().cpu() - ref.float()).abs().max().item()
+        assert err <= TOL_BF16, (i, err)
+
+
+def test_fp8_prefill_per_head_scales(gpu):
+    cfg = W.PrefillConfig("t", 1, 12, 2, 128, 64, 160, 128, 128, fp8=True, seed=77)
+    b = W.make_prefill_batch(cfg, gpu)
+    K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache, quant_mode=2,
+               k_scale=b.k_quant, v_scale=b.v_quant, scale_per_head=True)
+    q = b.q.transpose(0, 1).contiguous()
+    out = segmented_attention(q, b.k_cache, b.v_cache, b.block_table, b.prior.view(1, 1),
+                              cfg.block_size, 0, k_dequant_scale=b.k_dequant,
+                              v_dequant_scale=b.v_dequant)
+    # oracle: the reference semantics once per kv head with scalar folding
+    # (scale * s_k[h], output * s_v[h])
+    G = cfg.q_heads // cfg.kv_heads
+    for h in range(cfg.kv_heads):
+        sl = slice(h * G, (h + 1) * G)
+        kc = b.k_cache[:, h:h + 1].cpu().float()
+        vc = b.v_cache[:, h:h + 1].cpu().float()
+        ref = OSg.ref_segmented_attention(q[sl].cpu().float(), kc, vc, b.block_table.cpu(),
+                                          b.prior.cpu().view(1, 1), cfg.block_size,
+                                          cfg.head_dim ** -0.5 * float(b.k_dequant[h]))
+        ref = ref * float(b.v_dequant[h])
+        err = (out[sl].float().cpu() - ref).abs().max().item()
+        assert err <= TOL_FP8, (h, err)
+
+
+def test_mixed_batch_equals_composition(gpu):
+    """One mixed call (4 prefill chunks + decode rows) equals the reference
+    composition: segmented_attention per prefill sequence and the decode
+    path for the decode rows, over the same cache."""
+    pcfg = W.PrefillConfig("mp", 2, 16, 2, 128, 32, 96, 0, 300, seed=81)
+    pb = W.make_prefill_batch(pcfg, gpu)
+    dcfg = W.DecodeConfig("md", 3, 16, 2, 128, 32, 40, 500, seed=82)
+    db = W.make_decode_batch(dcfg, gpu)
+    # one cache pool: append the decode batch's blocks after the prefill's
+    nb_p = pb.k_cache.shape[0]
+    kc = torch.cat([pb.k_cache, db.k_cache], 0)
+    vc = torch.cat([pb.v_cache, db.v_cache], 0)
+    dt = torch.where(db.block_table >= 0, db.block_table + nb_p, db.block_table)
+    dslots = db.slots + nb_p * dcfg.block_size
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    out_d, out_p = mixed_batch_attention(
+        kc, vc, q_decode=db.q, k_decode=db.k_new, v_decode=db.v_new, decode_block_table=dt,
+        decode_pos_ids=db.pos, decode_slots=dslots, q_prefill=pb.q, k_prefill=pb.k_new,
+        v_prefill=pb.v_new, prefill_slots=pb.slots, prefill_cu_seqlens=pb.cu_seqlens,
+        prefill_prior=pb.prior, prefill_block_table=pb.block_table,
+        max_seqlen_q=pb.max_seqlen_q)
+    # composition, step by step
+    K.kv_write(pb.k_new, pb.v_new, pb.slots, kc_ref, vc_ref)
+    for i in range(pcfg.num_seqs):
+        s0, s1 = int(pb.cu_seqlens[i]), int(pb.cu_seqlens[i + 1])
+        q = pb.q[s0:s1].transpose(0, 1).contiguous()
+        ref = OSg.ref_segmented_attention(q.cpu(), kc_ref.cpu(), vc_ref.cpu(),
+                                          pb.block_table[i:i + 1].cpu(), pb.prior[i:i + 1].cpu(),
+                                          pcfg.block_size, pcfg.head_dim ** -0.5)
+        err = (out_p[s0:s1].transpose(0, 1).float().cpu() - ref.float()).abs().max().item()
+        assert err <= TOL_BF16, (i, err)
+    f = OD.fp32_decode(db.q.cpu(), db.k_new.cpu(), db.v_new.cpu(), kc_ref.cpu().float(),
+                       vc_ref.cpu().float(), dt.cpu(), db.pos.cpu(), scale=dcfg.head_dim ** -0.5)
+    err = (out_d.float().cpu().double() - f).abs().max().item()
+    assert err <= TOL_BF16, err
+    # the decode rows' new K/V landed in their slots
+    K.kv_write(db.k_new.reshape(-1, 2, 128), db.v_new.reshape(-1, 2, 128), dslots, kc_ref, vc_ref)
+    assert torch.equal(kc.cpu(), kc_ref.cpu()) and torch.equal(vc.cpu(), vc_ref.cpu())
+
+
+def test_prefill_empty_and_fully_masked(gpu):
+    """prior 0, window 1 (each row sees itself only) and a sequence of 0
+    rows in a varlen batch."""
+    cfg = W.PrefillConfig("t", 2, 8, 2, 64, 16, 40, 0, 0, seed=91)
+    b = W.make_prefill_batch(cfg, gpu)
+    K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache)
+    cu = torch.tensor([0, 40, 40], dtype=torch.int32, device=gpu)  # second sequence empty
+    out = K.paged_prefill(b.q[:40], cu, b.prior, 40, b.k_cache, b.v_cache, b.block_table,
+                          scale=64 ** -0.5, sliding_window=1)
+    # window 1: output row r = V[r] of its own kv head
+    v = _seq_kv(b.v_cache.cpu(), b.block_table[0].cpu(), 40, 2)  # [2, 40, 64]
+    ref = v.repeat_interleave(4, 0).transpose(0, 1)
+    assert (out.float().cpu() - ref.float()).abs().max().item() <= 1e-2

@@ -42,6 +42,7 @@ namespace {
 constexpr int kWaves = 4;
 constexpr int kTile = 64;  // tokens per wave tile
 constexpr int kPMax = 128;
+constexpr int kMaxSplitTokens = 4096;  // largest split-K chunk
 
 struct DecodeKParams {
   const uint16_t *q;
@@ -197,6 +198,7 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeKParams p) {
   __shared__ float p_lds[kWaves][kTile][NCP];
   __shared__ float a_lds[kWaves][16];
   __shared__ float red_lds[kWaves][NCP][D + 2];
+  __shared__ int32_t blk_lds[kMaxSplitTokens / 16 + 1];
 
   const int split = blockIdx.x;
   const int h = blockIdx.y;
@@ -250,46 +252,60 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeKParams p) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[c][e] = 0.f;
 
+  // Loads are unconditional: every address is taken from a wave-uniform,
+  // clamped group start inside [c_lo, c_hi) (so it lies in an attended,
+  // allocated block); rows outside the range are masked afterwards (scores
+  // to -inf, V rows to zero).  A predicated load would make the compiler
+  // wait for each load before writing the zero of the inactive lanes.
+  // Physical block ids of the chunk, staged once per workgroup in LDS (one
+  // vector load instead of a dependent scalar load per 16-token group).
+  const int cb0 = (int)fdiv((uint32_t)c_lo, p.bs_div);
+  const int cb1 = (int)fdiv((uint32_t)(c_hi - 1), p.bs_div);
+  for (int j = threadIdx.x; j <= cb1 - cb0; j += blockDim.x) {
+    int32_t v = p.bt[bt_row + (int64_t)(cb0 + j) * p.bt_j];
+    blk_lds[j] = v < 0 ? 0 : (v >= p.nb ? p.nb - 1 : v);
+  }
+  __syncthreads();
+
   const int chunk0 = split * p.split_tokens;
-  for (int t0 = chunk0 + wave * kTile; t0 < c_hi; t0 += kWaves * kTile) {
+  const int wv = readfirstlane(wave);
+  const int k_first = (c_lo >> 4) << 4, k_last = ((c_hi - 1) >> 4) << 4;
+  const int v_first = (c_lo / TL) * TL, v_last = ((c_hi - 1) / TL) * TL;
+  const uint8_t *kbase_h = p.k_cache + (int64_t)h * p.kc_h * EB;
+  const uint8_t *vbase_h = p.v_cache + (int64_t)h * p.vc_h * EB;
+  const int k_lane_off = (qcol * (int)p.kc_t + kg * 8) * EB;
+  const int v_lane_off = (tl * (int)p.vc_t + ds * 8) * EB;
+  for (int t0 = chunk0 + wv * kTile; t0 < c_hi; t0 += kWaves * kTile) {
     if (t0 + kTile <= c_lo) continue;  // uniform
+    // Every clamped group start below lies in [t0, t0 + 63] and in an
+    // attended block, so the tile needs at most 5 consecutive block ids:
+    // lane j holds block t0/bs + j (one LDS read per tile).
+    const int tb0 = (int)fdiv((uint32_t)t0, p.bs_div);
+    const int tile_blk = blk_lds[min(max(tb0 + lane - cb0, 0), cb1 - cb0)];
 
     // ---- K loads (A operand), 4 sub-tiles of 16 tokens
     raw_t kr[NSUB][KSTEPS];
 #pragma unroll
     for (int st = 0; st < NSUB; ++st) {
-      const int tb = t0 + st * 16;  // uniform, multiple of 16
-      const int tok = tb + qcol;
-      const bool ok = tok >= c_lo && tok < c_hi;
-      const uint32_t blk_i = fdiv((uint32_t)tb, p.bs_div);
-      int32_t phys = 0;
-      if (tb < c_hi) phys = p.bt[bt_row + (int64_t)blk_i * p.bt_j];
-      phys = phys < 0 ? 0 : (phys >= p.nb ? p.nb - 1 : phys);
-      const int in_blk = tb - (int)blk_i * p.bs + qcol;
-      const uint8_t *kp = p.k_cache +
-          ((int64_t)phys * p.kc_blk + (int64_t)h * p.kc_h +
-           (int64_t)in_blk * p.kc_t) * EB;
+      const int tb = min(max(t0 + st * 16, k_first), k_last);  // uniform
+      const int bi = (int)fdiv((uint32_t)tb, p.bs_div);
+      const int32_t phys = __builtin_amdgcn_readlane(tile_blk, bi - tb0);
+      const uint8_t *kp = kbase_h + ((int64_t)phys * p.kc_blk +
+                                     (int64_t)(tb - bi * p.bs) * p.kc_t) * EB;
 #pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks) {
-        kr[st][ks] = ok ? KL::load(kp + (ks * 32 + kg * 8) * EB) : KL::zero();
-      }
+      for (int ks = 0; ks < KSTEPS; ++ks)
+        kr[st][ks] = KL::load(kp + k_lane_off + ks * 32 * EB);
     }
     // ---- V loads (VALU layout)
     raw_t vr[VPL];
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      const int tb = t0 + i * TL;  // uniform
-      const int tok = tb + tl;
-      const bool ok = tok >= c_lo && tok < c_hi;
-      const uint32_t blk_i = fdiv((uint32_t)tb, p.bs_div);
-      int32_t phys = 0;
-      if (tb < c_hi) phys = p.bt[bt_row + (int64_t)blk_i * p.bt_j];
-      phys = phys < 0 ? 0 : (phys >= p.nb ? p.nb - 1 : phys);
-      const int in_blk = tb - (int)blk_i * p.bs + tl;
-      const uint8_t *vp = p.v_cache +
-          ((int64_t)phys * p.vc_blk + (int64_t)h * p.vc_h +
-           (int64_t)in_blk * p.vc_t + ds * 8) * EB;
-      vr[i] = ok ? KL::load(vp) : KL::zero();
+      const int tb = min(max(t0 + i * TL, v_first), v_last);  // uniform
+      const int bi = (int)fdiv((uint32_t)tb, p.bs_div);
+      const int32_t phys = __builtin_amdgcn_readlane(tile_blk, bi - tb0);
+      const uint8_t *vp = vbase_h + ((int64_t)phys * p.vc_blk +
+                                     (int64_t)(tb - bi * p.bs) * p.vc_t) * EB;
+      vr[i] = KL::load(vp + v_lane_off);
     }
 
     // ---- QK^T on MFMA
@@ -358,9 +374,14 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeKParams p) {
       for (int e = 0; e < 8; ++e) o[c][e] *= al[c];
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
-      float v[8];
-      v_to_f32<FP8>(vr[i], v);
       const int tloc = i * TL + tl;
+      const int tok = t0 + tloc;
+      const bool vok = tok >= c_lo && tok < c_hi;
+      raw_t r = vr[i];
+#pragma unroll
+      for (int w = 0; w < (int)(sizeof(raw_t) / 4); ++w) r[w] = vok ? r[w] : 0u;
+      float v[8];
+      v_to_f32<FP8>(r, v);
       float pc[NCP];
 #pragma unroll
       for (int c = 0; c < NCP; ++c) pc[c] = p_lds[wave][tloc][c];
@@ -600,6 +621,7 @@ DecodePlan plan_decode(const mia_decode_args &a) {
     while (st < want && st < 4096) st <<= 1;
   }
   st = ((st + kWaves * kTile - 1) / (kWaves * kTile)) * (kWaves * kTile);
+  if (st > kMaxSplitTokens) st = kMaxSplitTokens;  // block-id staging capacity
   pl.split_tokens = st;
   pl.num_splits = s_ctx > 0 ? (s_ctx + st - 1) / st : 0;
   if (pl.num_splits < 1) pl.num_splits = 1;
@@ -660,6 +682,11 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
 
   const dim3 grid((unsigned)pl.num_splits, (unsigned)a.num_kv_heads,
                   (unsigned)a.batch);
+  if (a.split_event_begin) {
+    int rc = check_hip(hipEventRecord((hipEvent_t)a.split_event_begin, s),
+                       "decode: timing event");
+    if (rc) return rc;
+  }
   if (pl.num_splits > 0 && kp.s_ctx - kp.S > 0) {
     for (int cg = 0; cg < pl.col_groups; ++cg) {
       kp.col0 = cg * 16;
@@ -674,6 +701,11 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
       int rc = check_hip(hipGetLastError(), "decode split launch");
       if (rc) return rc;
     }
+  }
+  if (a.split_event_end) {
+    int rc = check_hip(hipEventRecord((hipEvent_t)a.split_event_end, s),
+                       "decode: timing event");
+    if (rc) return rc;
   }
   kp.col0 = 0;
   CombineParams cp;

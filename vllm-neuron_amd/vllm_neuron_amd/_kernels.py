@@ -243,6 +243,7 @@ def paged_decode(
     out: Optional[torch.Tensor] = None,
     workspace: Optional[torch.Tensor] = None,
     split_tokens: int = 0,
+    split_events: Optional[tuple] = None,
 ) -> torch.Tensor:
     """Attention of ``q [B, S, Hq, d]`` over the paged prior context plus the
     active rows ``k_new/v_new [B, S, Hkv, d]``; returns ``[B, S, Hq, d]`` bf16.
@@ -337,6 +338,11 @@ def paged_decode(
     a.out = out.data_ptr()
     a.out_stride = _arr(ctypes.c_int64, list(out.stride()))
     a.split_tokens = split_tokens
+    if split_events is not None:
+        # torch events (already created on this device) timing the split-K
+        # kernels alone
+        a.split_event_begin = split_events[0].cuda_event
+        a.split_event_end = split_events[1].cuda_event
     L = N.lib()
     need = L.mia_decode_workspace_bytes(ctypes.byref(a))
     if need == 0:

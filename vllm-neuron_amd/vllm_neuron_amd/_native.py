@@ -98,6 +98,7 @@ class DecodeArgs(ctypes.Structure):
         ("out", c_vp), ("out_stride", c_i64 * 4),
         ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t),
         ("split_tokens", c_i32), ("_pad1", c_i32),
+        ("split_event_begin", c_vp), ("split_event_end", c_vp),
     ]
 
 

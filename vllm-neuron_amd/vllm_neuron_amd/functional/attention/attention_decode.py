@@ -380,6 +380,7 @@ def paged_decode_core(
     v_dequant_scale: Optional[Tensor] = None,
     workspace: Optional[Tensor] = None,
     split_tokens: int = 0,
+    split_events: Optional[tuple] = None,
 ) -> Tensor:
     """Attention core of stages 7a-7g: ``q [B, S, Hq, d]`` attends to the
     paged prior context and the active rows ``k_new/v_new [B, S, Hkv, d]``
@@ -396,7 +397,7 @@ def paged_decode_core(
 
     kw = dict(softmax_scale=softmax_scale, sink=sink,
               k_dequant=k_dequant_scale, v_dequant=v_dequant_scale,
-              workspace=workspace, split_tokens=split_tokens)
+              workspace=workspace, split_tokens=split_tokens, split_events=split_events)
     if k_scale is not None:
         kw["quant_mode"] = _quant_mode_for(k_new.dtype, k_scale)
         kw["k_quant"] = k_scale
