@@ -126,6 +126,8 @@ static int validate_decode(const mia_decode_args *a) {
   MIA_REQUIRE(a->batch > 0 && a->s_active > 0 && a->num_q_heads > 0 &&
                   a->num_kv_heads > 0,
               MIA_ERR_VALUE, "decode: bad shape");
+  MIA_REQUIRE(a->batch <= 1024, MIA_ERR_NOT_IMPLEMENTED,
+              "decode: at most 1024 batch rows per call");
   MIA_REQUIRE(a->num_q_heads % a->num_kv_heads == 0, MIA_ERR_VALUE,
               "GQA requires q_heads divisible by kv_heads");
   MIA_REQUIRE(a->head_dim == 64 || a->head_dim == 128, MIA_ERR_NOT_IMPLEMENTED,

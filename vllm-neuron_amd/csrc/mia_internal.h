@@ -36,6 +36,7 @@ struct DecodePlan {
   int num_splits;    // ceil(S_ctx / split_tokens)
   int ncols;         // columns (query token x head of a GQA group) per launch
   int col_groups;    // launches over column groups
+  int grid;          // workgroups of the persistent split-K kernel
   size_t ws_bytes;   // workspace bytes
 };
 DecodePlan plan_decode(const mia_decode_args &a);

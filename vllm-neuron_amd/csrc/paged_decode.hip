@@ -40,9 +40,26 @@ namespace mia {
 namespace {
 
 constexpr int kWaves = 4;
-constexpr int kTile = 64;  // tokens per wave tile
+constexpr int kTile = 32;  // tokens per wave tile
 constexpr int kPMax = 128;
-constexpr int kMaxSplitTokens = 4096;  // largest split-K chunk
+constexpr int kMaxSplitTokens = 1024;  // largest chunk (block ids of a chunk fit a wave)
+constexpr int kDefaultChunk = 256;     // tokens per work item
+constexpr int kMaxRows = 1024;         // batch rows of the persistent decode
+
+// Compute units of the current device (queried once per device).
+int device_cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
 
 struct DecodeKParams {
   const uint16_t *q;
@@ -66,6 +83,7 @@ struct DecodeKParams {
   const float *k_deq;
   int split_tokens;
   int num_splits;
+  int nblk;  // block-table width
   int col0;    // first column of this launch
   int nc_tot;  // G * S
   float *ws_o;   // [B, Hkv, num_splits, nc_tot, D]
@@ -184,6 +202,23 @@ MIA_DEV void v_to_f32<true>(u32x2_t r, float v[8]) {
 // ---------------------------------------------------------------------------
 // split kernel
 // ---------------------------------------------------------------------------
+// One work item of a streaming wave: kv head h of batch row b, chunk c
+// (tokens [c*CH, (c+1)*CH) of the prior range).  All fields are wave
+// uniform.
+struct Item {
+  int valid, b, h, c, t_lo, t_hi, cb0;
+  float minpos;
+};
+
+MIA_DEV int wave_scan_incl(int x, int lane) {
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off, 64);
+    if (lane >= off) x += y;
+  }
+  return x;
+}
+
 template <int D, int NCP, bool FP8>
 __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeKParams p) {
   constexpr int EB = FP8 ? 1 : 2;      // cache element bytes
@@ -197,253 +232,314 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeKParams p) {
 
   __shared__ float p_lds[kWaves][kTile][NCP];
   __shared__ float a_lds[kWaves][16];
-  __shared__ float red_lds[kWaves][NCP][D + 2];
-  __shared__ int32_t blk_lds[kMaxSplitTokens / 16 + 1];
+  __shared__ int s_item0[kMaxRows + 1];
+  __shared__ int s_lo[kMaxRows];
+  __shared__ int s_hi[kMaxRows];
+  __shared__ float s_minpos[kMaxRows];
 
-  const int split = blockIdx.x;
-  const int h = blockIdx.y;
-  const int b = blockIdx.z;
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
+  const int CH = p.split_tokens;
 
-  const RowInfo ri = row_info(p.pos, p.start, p.mask_mode, p.S, p.s_ctx, b);
-  const int c_lo = max(ri.lo, split * p.split_tokens);
-  const int c_hi = min(ri.hi, (split + 1) * p.split_tokens);
-  if (c_lo >= c_hi) return;  // uniform over the workgroup
+  // ---- setup (every workgroup): prior range of each row and the prefix
+  // sum of work items (rows x kv heads x chunks overlapping the range)
+  for (int r = threadIdx.x; r < p.B; r += blockDim.x) {
+    const RowInfo ri = row_info(p.pos, p.start, p.mask_mode, p.S, p.s_ctx, r);
+    s_lo[r] = ri.lo;
+    s_hi[r] = ri.hi;
+    s_minpos[r] = ri.minpos;
+  }
+  __syncthreads();
+  if (wave == 0) {
+    int carry = 0;
+    if (lane == 0) s_item0[0] = 0;
+    for (int r0 = 0; r0 < p.B; r0 += 64) {
+      const int r = r0 + lane;
+      int n = 0;
+      if (r < p.B && s_lo[r] < s_hi[r]) n = ((s_hi[r] - 1) / CH - s_lo[r] / CH + 1) * p.Hkv;
+      const int incl = wave_scan_incl(n, lane) + carry;
+      if (r < p.B) s_item0[r + 1] = incl;
+      carry = __shfl(incl, 63, 64);
+    }
+  }
+  __syncthreads();
+  const int n_items = s_item0[p.B];
+  const int n_workers = gridDim.x * kWaves;
+  int item_id = readfirstlane(blockIdx.x * kWaves + wave);
+  if (item_id >= n_items) return;  // no barrier below this point
 
-  // ---- query column owned by this lane in the QK layout
+  // ---- lane roles
   const int qcol = lane & 15;
   const int kg = lane >> 4;  // k-group (8 d-values) / token quad
   const int gcol = p.col0 + qcol;
   const bool col_ok = (qcol < NCP) && (gcol < p.nc_tot);
   const int s_q = col_ok ? gcol / p.G : 0;
-  const int hq = h * p.G + (col_ok ? gcol % p.G : 0);
-  float st_q = 0.f;
-  bool wrap_q = false;
-  if (p.mask_mode == 0 && p.start && col_ok) {
-    st_q = p.start[(int64_t)b * p.S + s_q];
-    wrap_q = st_q > ri.minpos;
-  }
-
-  bf16x8_t qf[KSTEPS];
-  {
-    const uint16_t *qp = p.q + b * p.qs_b + (int64_t)s_q * p.qs_s + hq * p.qs_h;
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) {
-      u32x4_t w = {0u, 0u, 0u, 0u};
-      if (col_ok)
-        w = *reinterpret_cast<const u32x4_t *>(qp + ks * 32 + kg * 8);
-      qf[ks] = __builtin_bit_cast(bf16x8_t, w);
-    }
-  }
-
-  const float scale2 = p.scale_log2 * (p.k_deq ? p.k_deq[h] : 1.0f);
-  const int64_t bt_row = (int64_t)b * p.bt_b + (int64_t)h * p.bt_h;
-
-  // PV lane roles
-  const int ds = lane % DS;
+  const int g_q = col_ok ? gcol % p.G : 0;
+  const int ds = lane % DS;  // PV lane roles
   const int tl = lane / DS;
-
-  float m_run = -INFINITY;  // per column (lane & 15)
-  float l_run = 0.f;        // per lane partial
-  float o[NCP][8];
-#pragma unroll
-  for (int c = 0; c < NCP; ++c)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) o[c][e] = 0.f;
-
-  // Loads are unconditional: every address is taken from a wave-uniform,
-  // clamped group start inside [c_lo, c_hi) (so it lies in an attended,
-  // allocated block); rows outside the range are masked afterwards (scores
-  // to -inf, V rows to zero).  A predicated load would make the compiler
-  // wait for each load before writing the zero of the inactive lanes.
-  // Physical block ids of the chunk, staged once per workgroup in LDS (one
-  // vector load instead of a dependent scalar load per 16-token group).
-  const int cb0 = (int)fdiv((uint32_t)c_lo, p.bs_div);
-  const int cb1 = (int)fdiv((uint32_t)(c_hi - 1), p.bs_div);
-  for (int j = threadIdx.x; j <= cb1 - cb0; j += blockDim.x) {
-    int32_t v = p.bt[bt_row + (int64_t)(cb0 + j) * p.bt_j];
-    blk_lds[j] = v < 0 ? 0 : (v >= p.nb ? p.nb - 1 : v);
-  }
-  __syncthreads();
-
-  const int chunk0 = split * p.split_tokens;
-  const int wv = readfirstlane(wave);
-  const int k_first = (c_lo >> 4) << 4, k_last = ((c_hi - 1) >> 4) << 4;
-  const int v_first = (c_lo / TL) * TL, v_last = ((c_hi - 1) / TL) * TL;
-  const uint8_t *kbase_h = p.k_cache + (int64_t)h * p.kc_h * EB;
-  const uint8_t *vbase_h = p.v_cache + (int64_t)h * p.vc_h * EB;
   const int k_lane_off = (qcol * (int)p.kc_t + kg * 8) * EB;
   const int v_lane_off = (tl * (int)p.vc_t + ds * 8) * EB;
-  for (int t0 = chunk0 + wv * kTile; t0 < c_hi; t0 += kWaves * kTile) {
-    if (t0 + kTile <= c_lo) continue;  // uniform
-    // Every clamped group start below lies in [t0, t0 + 63] and in an
-    // attended block, so the tile needs at most 5 consecutive block ids:
-    // lane j holds block t0/bs + j (one LDS read per tile).
-    const int tb0 = (int)fdiv((uint32_t)t0, p.bs_div);
-    const int tile_blk = blk_lds[min(max(tb0 + lane - cb0, 0), cb1 - cb0)];
+  const int max_blk = CH / 16 + 1;  // block ids a chunk can touch (<= 64)
 
-    // ---- K loads (A operand), 4 sub-tiles of 16 tokens
-    raw_t kr[NSUB][KSTEPS];
+  // Item id -> (b, h, c) by binary search over the prefix sum; an id past
+  // the end yields `fallback` with valid = 0 (so its loads stay in bounds).
+  auto decode_item = [&](int id, const Item &fallback) {
+    Item it;
+    if (id >= n_items) {
+      it = fallback;
+      it.valid = 0;
+      return it;
+    }
+    int lo = 0, hi = p.B;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (s_item0[mid] <= id) lo = mid; else hi = mid;
+    }
+    const int b = readfirstlane(lo);
+    const int r = id - readfirstlane(s_item0[b]);
+    const int n_b = (readfirstlane(s_item0[b + 1]) - readfirstlane(s_item0[b])) / p.Hkv;
+    const int row_lo = readfirstlane(s_lo[b]);
+    const int row_hi = readfirstlane(s_hi[b]);
+    it.valid = 1;
+    it.b = b;
+    it.h = r / n_b;
+    it.c = row_lo / CH + (r - it.h * n_b);
+    it.t_lo = max(row_lo, it.c * CH);
+    it.t_hi = min(row_hi, it.c * CH + CH);
+    it.cb0 = (int)fdiv((uint32_t)(it.c * CH), p.bs_div);
+    it.minpos = __builtin_bit_cast(float, readfirstlane(__builtin_bit_cast(int, s_minpos[b])));
+    return it;
+  };
+  // Per-item vector data: block ids (lane j = block cb0 + j), Q columns,
+  // sliding-window start of this lane's column.
+  auto load_blocks = [&](const Item &it) {
+    const int n = min(max_blk, p.nblk - it.cb0);
+    const int j = min(lane, n - 1);
+    int32_t v = p.bt[(int64_t)it.b * p.bt_b + (int64_t)it.h * p.bt_h +
+                     (int64_t)(it.cb0 + j) * p.bt_j];
+    return v < 0 ? 0 : (v >= p.nb ? p.nb - 1 : v);
+  };
+  auto load_q = [&](const Item &it, bf16x8_t (&qf)[KSTEPS]) {
+    const uint16_t *qp = p.q + it.b * p.qs_b + (int64_t)s_q * p.qs_s +
+                         (int64_t)(it.h * p.G + g_q) * p.qs_h;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      u32x4_t w = *reinterpret_cast<const u32x4_t *>(qp + ks * 32 + kg * 8);
+      if (!col_ok) w = u32x4_t{0u, 0u, 0u, 0u};
+      qf[ks] = __builtin_bit_cast(bf16x8_t, w);
+    }
+  };
+  auto load_start = [&](const Item &it) {
+    return (p.mask_mode == 0 && p.start) ? p.start[(int64_t)it.b * p.S + s_q] : 0.f;
+  };
+
+  // Loads are unconditional: every address is taken from a wave-uniform,
+  // clamped group start inside [t_lo, t_hi) of the item (so it lies in an
+  // attended, allocated block); rows outside the range are masked
+  // afterwards (scores to -inf, V rows to zero).  A predicated load would
+  // make the compiler wait for each load before writing the zero of the
+  // inactive lanes.
+  auto issue_k = [&](raw_t (&kr)[NSUB][KSTEPS], const Item &it, int blk, int t0) {
+    const int k_first = (it.t_lo >> 4) << 4, k_last = ((it.t_hi - 1) >> 4) << 4;
+    const uint8_t *kbase = p.k_cache + (int64_t)it.h * p.kc_h * EB;
 #pragma unroll
     for (int st = 0; st < NSUB; ++st) {
       const int tb = min(max(t0 + st * 16, k_first), k_last);  // uniform
       const int bi = (int)fdiv((uint32_t)tb, p.bs_div);
-      const int32_t phys = __builtin_amdgcn_readlane(tile_blk, bi - tb0);
-      const uint8_t *kp = kbase_h + ((int64_t)phys * p.kc_blk +
-                                     (int64_t)(tb - bi * p.bs) * p.kc_t) * EB;
+      const int32_t phys = __builtin_amdgcn_readlane(blk, bi - it.cb0);
+      const uint8_t *kp = kbase + ((int64_t)phys * p.kc_blk +
+                                   (int64_t)(tb - bi * p.bs) * p.kc_t) * EB;
 #pragma unroll
       for (int ks = 0; ks < KSTEPS; ++ks)
         kr[st][ks] = KL::load(kp + k_lane_off + ks * 32 * EB);
     }
-    // ---- V loads (VALU layout)
-    raw_t vr[VPL];
+  };
+  auto issue_v = [&](raw_t (&vr)[VPL], const Item &it, int blk, int t0) {
+    const int v_first = (it.t_lo / TL) * TL, v_last = ((it.t_hi - 1) / TL) * TL;
+    const uint8_t *vbase = p.v_cache + (int64_t)it.h * p.vc_h * EB;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
       const int tb = min(max(t0 + i * TL, v_first), v_last);  // uniform
       const int bi = (int)fdiv((uint32_t)tb, p.bs_div);
-      const int32_t phys = __builtin_amdgcn_readlane(tile_blk, bi - tb0);
-      const uint8_t *vp = vbase_h + ((int64_t)phys * p.vc_blk +
-                                     (int64_t)(tb - bi * p.bs) * p.vc_t) * EB;
+      const int32_t phys = __builtin_amdgcn_readlane(blk, bi - it.cb0);
+      const uint8_t *vp = vbase + ((int64_t)phys * p.vc_blk +
+                                   (int64_t)(tb - bi * p.bs) * p.vc_t) * EB;
       vr[i] = KL::load(vp + v_lane_off);
     }
+  };
+  auto first_tile = [&](const Item &it) { return (it.t_lo / kTile) * kTile; };
 
-    // ---- QK^T on MFMA
-    float sc[NSUB][4];
-#pragma unroll
-    for (int st = 0; st < NSUB; ++st) {
-      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(KL::to_bf16(kr[st][ks]),
-                                                      qf[ks], acc, 0, 0, 0);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int tok = t0 + st * 16 + kg * 4 + i;
-        bool ok = col_ok && tok >= c_lo && tok < c_hi;
-        if (ok) {
-          if (p.mask_mode == 1) {
-            const int64_t lin = seq_to_linear(tok, p.mask_bl);
-            const int64_t mi = ((lin * p.B + b) * p.Hq + hq) * p.S + s_q;
-            ok = p.full_mask[mi] != 0.f;
-          } else if (p.start) {
-            const float ft = (float)tok;
-            ok = wrap_q ? (ft >= st_q || ft < ri.minpos)
-                        : (ft >= st_q && ft < ri.minpos);
-          }
-        }
-        sc[st][i] = ok ? acc[i] * scale2 : -INFINITY;
-      }
-    }
+  // ---- the stream: this wave's items (every n_workers-th), tile after
+  // tile; the next tile's K (V) loads are issued as soon as QK (PV) has
+  // consumed the registers, across item boundaries, so one tile of loads
+  // is always in flight.  Past the last item the prefetch re-reads the
+  // current tile (an L2 hit): no load is conditional.
+  Item cur = decode_item(item_id, Item{});
+  int blk_cur = load_blocks(cur);
+  bf16x8_t q_cur[KSTEPS];
+  load_q(cur, q_cur);
+  float st_cur = load_start(cur);
+  raw_t kr[NSUB][KSTEPS];
+  raw_t vr[VPL];
+  issue_k(kr, cur, blk_cur, first_tile(cur));
+  issue_v(vr, cur, blk_cur, first_tile(cur));
+  const float kdeq_all = 1.0f;
+  (void)kdeq_all;
 
-    // ---- online softmax (exp2 domain)
-    float mx = -INFINITY;
-#pragma unroll
-    for (int st = 0; st < NSUB; ++st)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[st][i]);
-    mx = wave_max_xor(mx, 16);
-    mx = wave_max_xor(mx, 32);
-    const float m_new = fmaxf(m_run, mx);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    m_run = m_new;
-    float psum = 0.f;
-#pragma unroll
-    for (int st = 0; st < NSUB; ++st) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float pv = __builtin_amdgcn_exp2f(sc[st][i] - m_use);
-        psum += pv;
-        if (qcol < NCP) p_lds[wave][st * 16 + kg * 4 + i][qcol] = pv;
-      }
-    }
-    l_run = l_run * alpha + psum;
-    if (lane < 16) a_lds[wave][lane] = alpha;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  while (true) {
+    const Item nxt = decode_item(item_id + n_workers, cur);
+    const int blk_nxt = load_blocks(nxt);
+    bf16x8_t q_nxt[KSTEPS];
+    load_q(nxt, q_nxt);
+    const float st_nxt = load_start(nxt);
 
-    // ---- PV on the vector ALU
-    float al[NCP];
-#pragma unroll
-    for (int c = 0; c < NCP; ++c) al[c] = a_lds[wave][c];
+    const float scale2 = p.scale_log2 * (p.k_deq ? p.k_deq[cur.h] : 1.0f);
+    const bool wrap_q = st_cur > cur.minpos;
+    float m_run = -INFINITY;  // per column (lane & 15)
+    float l_run = 0.f;        // per lane partial
+    float o[NCP][8];
 #pragma unroll
     for (int c = 0; c < NCP; ++c)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[c][e] *= al[c];
+      for (int e = 0; e < 8; ++e) o[c][e] = 0.f;
+
+    const int t_first = first_tile(cur);
+    for (int t0 = t_first; t0 < cur.t_hi; t0 += kTile) {
+      // target of the prefetch issued during this tile (uniform selects)
+      const bool last = t0 + kTile >= cur.t_hi;
+      const bool to_next = last && nxt.valid;
+      const Item &itN = to_next ? nxt : cur;
+      const int blkN = to_next ? blk_nxt : blk_cur;
+      const int tN = to_next ? first_tile(nxt) : (last ? t0 : t0 + kTile);
+
+      // ---- QK^T on MFMA
+      float sc[NSUB][4];
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const int tloc = i * TL + tl;
-      const int tok = t0 + tloc;
-      const bool vok = tok >= c_lo && tok < c_hi;
-      raw_t r = vr[i];
+      for (int st = 0; st < NSUB; ++st) {
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int w = 0; w < (int)(sizeof(raw_t) / 4); ++w) r[w] = vok ? r[w] : 0u;
-      float v[8];
-      v_to_f32<FP8>(r, v);
-      float pc[NCP];
+        for (int ks = 0; ks < KSTEPS; ++ks)
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(KL::to_bf16(kr[st][ks]),
+                                                        q_cur[ks], acc, 0, 0, 0);
 #pragma unroll
-      for (int c = 0; c < NCP; ++c) pc[c] = p_lds[wave][tloc][c];
+        for (int i = 0; i < 4; ++i) sc[st][i] = acc[i];
+      }
+      issue_k(kr, itN, blkN, tN);
+#pragma unroll
+      for (int st = 0; st < NSUB; ++st) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int tok = t0 + st * 16 + kg * 4 + i;
+          bool ok = col_ok && tok >= cur.t_lo && tok < cur.t_hi;
+          if (ok) {
+            if (p.mask_mode == 1) {
+              const int hq = cur.h * p.G + g_q;
+              const int64_t lin = seq_to_linear(tok, p.mask_bl);
+              const int64_t mi = ((lin * p.B + cur.b) * p.Hq + hq) * p.S + s_q;
+              ok = p.full_mask[mi] != 0.f;
+            } else if (p.start) {
+              const float ft = (float)tok;
+              ok = wrap_q ? (ft >= st_cur || ft < cur.minpos)
+                          : (ft >= st_cur && ft < cur.minpos);
+            }
+          }
+          sc[st][i] = ok ? sc[st][i] * scale2 : -INFINITY;
+        }
+      }
+      // ---- online softmax (exp2 domain)
+      float mx = -INFINITY;
+#pragma unroll
+      for (int st = 0; st < NSUB; ++st)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[st][i]);
+      mx = wave_max_xor(mx, 16);
+      mx = wave_max_xor(mx, 32);
+      const float m_new = fmaxf(m_run, mx);
+      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      m_run = m_new;
+      float psum = 0.f;
+#pragma unroll
+      for (int st = 0; st < NSUB; ++st) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float pv = __builtin_amdgcn_exp2f(sc[st][i] - m_use);
+          psum += pv;
+          if (qcol < NCP) p_lds[wave][st * 16 + kg * 4 + i][qcol] = pv;
+        }
+      }
+      l_run = l_run * alpha + psum;
+      if (lane < 16) a_lds[wave][lane] = alpha;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+      // ---- PV on the vector ALU
+      float al[NCP];
+#pragma unroll
+      for (int c = 0; c < NCP; ++c) al[c] = a_lds[wave][c];
 #pragma unroll
       for (int c = 0; c < NCP; ++c)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[c][e] = fmaf(pc[c], v[e], o[c][e]);
+        for (int e = 0; e < 8; ++e) o[c][e] *= al[c];
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        const int tloc = i * TL + tl;
+        const int tok = t0 + tloc;
+        const bool vok = tok >= cur.t_lo && tok < cur.t_hi;
+        raw_t rv = vr[i];
+#pragma unroll
+        for (int w = 0; w < (int)(sizeof(raw_t) / 4); ++w) rv[w] = vok ? rv[w] : 0u;
+        float v[8];
+        v_to_f32<FP8>(rv, v);
+        float pc[NCP];
+#pragma unroll
+        for (int c = 0; c < NCP; ++c) pc[c] = p_lds[wave][tloc][c];
+#pragma unroll
+        for (int c = 0; c < NCP; ++c)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) o[c][e] = fmaf(pc[c], v[e], o[c][e]);
+      }
+      issue_v(vr, itN, blkN, tN);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-  }
 
-  // ---- reduce within the wave
-  l_run = wave_sum_xor(l_run, 16);
-  l_run = wave_sum_xor(l_run, 32);
-#pragma unroll
-  for (int c = 0; c < NCP; ++c)
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      float x = o[c][e];
-#pragma unroll
-      for (int msk = DS; msk < 64; msk <<= 1) x = wave_sum_xor(x, msk);
-      o[c][e] = x;
-    }
-
-  // ---- merge the waves through LDS
-  if (lane < NCP) {
-    red_lds[wave][lane][D] = m_run;
-    red_lds[wave][lane][D + 1] = l_run;
-  }
-  if (tl == 0) {
+    // ---- item epilogue: reduce within the wave, write the partial
+    l_run = wave_sum_xor(l_run, 16);
+    l_run = wave_sum_xor(l_run, 32);
 #pragma unroll
     for (int c = 0; c < NCP; ++c)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) red_lds[wave][c][ds * 8 + e] = o[c][e];
-  }
-  __syncthreads();
+      for (int e = 0; e < 8; ++e) {
+        float x = o[c][e];
+#pragma unroll
+        for (int msk = DS; msk < 64; msk <<= 1) x = wave_sum_xor(x, msk);
+        o[c][e] = x;
+      }
+    const int64_t ws_row = (((int64_t)cur.b * p.Hkv + cur.h) * p.num_splits + cur.c) * p.nc_tot;
+    if (tl == 0) {
+#pragma unroll
+      for (int c = 0; c < NCP; ++c) {
+        if (p.col0 + c < p.nc_tot) {
+          float *dst = p.ws_o + (ws_row + p.col0 + c) * D + ds * 8;
+          *reinterpret_cast<f32x4_t *>(dst) = f32x4_t{o[c][0], o[c][1], o[c][2], o[c][3]};
+          *reinterpret_cast<f32x4_t *>(dst + 4) = f32x4_t{o[c][4], o[c][5], o[c][6], o[c][7]};
+        }
+      }
+    }
+    if (lane < NCP && p.col0 + lane < p.nc_tot) {
+      p.ws_ml[(ws_row + p.col0 + lane) * 2] = m_run;
+      p.ws_ml[(ws_row + p.col0 + lane) * 2 + 1] = l_run;
+    }
 
-  const int64_t ws_row =
-      (((int64_t)b * p.Hkv + h) * p.num_splits + split) * p.nc_tot;
-  for (int idx = threadIdx.x; idx < NCP * D; idx += blockDim.x) {
-    const int c = idx / D;
-    const int d = idx % D;
-    const int gc = p.col0 + c;
-    if (gc >= p.nc_tot) continue;
-    float M = -INFINITY;
+    if (!nxt.valid) break;
+    item_id += n_workers;
+    cur = nxt;
+    blk_cur = blk_nxt;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, red_lds[w][c][D]);
-    const float Mu = (M == -INFINITY) ? 0.f : M;
-    float acc = 0.f, L = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float wt = __builtin_amdgcn_exp2f(red_lds[w][c][D] - Mu);
-      acc += red_lds[w][c][d] * wt;
-      L += red_lds[w][c][D + 1] * wt;
-    }
-    p.ws_o[(ws_row + gc) * D + d] = acc;
-    if (d == 0) {
-      p.ws_ml[(ws_row + gc) * 2] = M;
-      p.ws_ml[(ws_row + gc) * 2 + 1] = L;
-    }
+    for (int ks = 0; ks < KSTEPS; ++ks) q_cur[ks] = q_nxt[ks];
+    st_cur = st_nxt;
   }
 }
 
@@ -610,23 +706,25 @@ DecodePlan plan_decode(const mia_decode_args &a) {
   DecodePlan pl;
   const int G = a.num_q_heads / a.num_kv_heads;
   const int s_ctx = a.blocks_per_seq * a.block_size;
-  int st = a.split_tokens;
-  if (st <= 0) {
-    // Shape-only choice (graph-capturable, no host sync): aim for ~8k
-    // workgroups over the worst case B*Hkv*S_ctx, chunks of 256..4096
-    // tokens in powers of two.
-    const int64_t work = (int64_t)a.batch * a.num_kv_heads * s_ctx;
-    int64_t want = work / 8192;
-    st = 256;
-    while (st < want && st < 4096) st <<= 1;
-  }
-  st = ((st + kWaves * kTile - 1) / (kWaves * kTile)) * (kWaves * kTile);
-  if (st > kMaxSplitTokens) st = kMaxSplitTokens;  // block-id staging capacity
+  // Work items are (row, kv head, chunk of split_tokens tokens); each is
+  // streamed by one wave.  The chunk is a shape-only choice (graph
+  // capturable, no host sync), a multiple of the 32-token tile whose block
+  // ids fit in one wave register.
+  int st = a.split_tokens > 0 ? a.split_tokens : kDefaultChunk;
+  st = ((st + kTile - 1) / kTile) * kTile;
+  const int st_cap = std::min(kMaxSplitTokens, (63 * a.block_size / kTile) * kTile);
+  if (st > st_cap) st = st_cap;
   pl.split_tokens = st;
   pl.num_splits = s_ctx > 0 ? (s_ctx + st - 1) / st : 0;
   if (pl.num_splits < 1) pl.num_splits = 1;
   pl.ncols = G * a.s_active;
   pl.col_groups = (pl.ncols + 15) / 16;
+  // persistent grid: two workgroups of four streaming waves per CU, or
+  // fewer when the worst-case item count is smaller
+  const int64_t max_items = (int64_t)a.batch * a.num_kv_heads * pl.num_splits;
+  int64_t wg = (max_items + kWaves - 1) / kWaves;
+  const int64_t cap = 2 * (int64_t)device_cu_count();
+  pl.grid = (int)std::max<int64_t>(1, std::min(wg, cap));
   const size_t rows = (size_t)a.batch * a.num_kv_heads * pl.num_splits * pl.ncols;
   size_t o_bytes = rows * (size_t)a.head_dim * sizeof(float);
   o_bytes = (o_bytes + 255) & ~(size_t)255;
@@ -672,6 +770,7 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
   kp.scale_log2 = a.softmax_scale * kLog2e * (fp8 ? 256.0f : 1.0f);
   kp.k_deq = a.k_dequant;
   kp.split_tokens = pl.split_tokens;
+  kp.nblk = a.blocks_per_seq;
   kp.num_splits = pl.num_splits;
   kp.nc_tot = pl.ncols;
   const size_t rows = (size_t)a.batch * a.num_kv_heads * pl.num_splits * pl.ncols;
@@ -680,8 +779,7 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
   kp.ws_o = (float *)a.workspace;
   kp.ws_ml = (float *)((char *)a.workspace + o_bytes);
 
-  const dim3 grid((unsigned)pl.num_splits, (unsigned)a.num_kv_heads,
-                  (unsigned)a.batch);
+  const dim3 grid((unsigned)pl.grid);
   if (a.split_event_begin) {
     int rc = check_hip(hipEventRecord((hipEvent_t)a.split_event_begin, s),
                        "decode: timing event");
