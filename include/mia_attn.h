@@ -244,6 +244,14 @@ typedef struct {
    * (the combine kernel is outside).  NULL = not recorded. */
   void *split_event_begin;
   void *split_event_end;
+  /* Optional fused cache update (stage 8 of the reference decode): when
+   * non-NULL, the S active K/V rows of batch row b are written to slot
+   * write_slots[b * S + s] of k_cache / v_cache after attention has read the
+   * cache (quantised with k_quant / v_quant for an FP8 cache).  Slots
+   * outside [0, num_blocks * block_size) are skipped.  I32 / I64 / U32. */
+  const void *write_slots;
+  int32_t write_slot_dtype;
+  int32_t _pad2;
 } mia_decode_args;
 
 size_t mia_decode_workspace_bytes(const mia_decode_args *args);

@@ -225,3 +225,37 @@ def test_c5_fp8_full_size(gpu):
     ref = _fp32(b, cfg.head_dim ** -0.5)
     err = (out.double() - ref).abs().max().item()
     assert err <= TOL_FP8, err
+
+
+@pytest.mark.parametrize("case", [0, 7, 8])
+@pytest.mark.parametrize("S", [1, 3])
+def test_fused_cache_write_matches_scatter(gpu, case, S):
+    """The cache update fused into the decode launch writes the same bytes as
+    the standalone scatter (mia_kv_write), including FP8 quantisation, and
+    skips sentinel slots; the attention output is unchanged by it."""
+    from vllm_neuron_amd import _kernels as K
+    cfg = _small_cfg(**CASES[case])
+    b = _make(cfg, gpu, S=S)
+    B, Hkv = cfg.batch, cfg.kv_heads
+    nb, bs = b.k_cache.shape[0], cfg.block_size
+    g = torch.Generator().manual_seed(11)
+    slots = torch.randperm(nb * bs, generator=g)[:B * S].to(torch.int64)
+    slots[0] = -1                      # sentinel: skipped
+    slots[-1] = nb * bs + 5            # beyond the pool: skipped
+    slots = slots.to(gpu)
+    kc, vc = b.k_cache.clone(), b.v_cache.clone()
+    base = _run_core(b)
+    fused = _run_core(b, write_slots=slots)
+    assert torch.equal(base, fused)
+    # standalone scatter on the untouched copies
+    kw = {}
+    if cfg.fp8:
+        from vllm_neuron_amd.functional.attention.attention_decode import (
+            _quant_mode_for, _scale_per_head)
+        kw = dict(quant_mode=_quant_mode_for(b.k_new.dtype, b.k_quant), k_scale=b.k_quant,
+                  v_scale=b.v_quant, scale_per_head=_scale_per_head(b.k_quant, Hkv))
+    K.kv_write(b.k_new.reshape(B * S, Hkv, -1), b.v_new.reshape(B * S, Hkv, -1), slots, kc, vc,
+               **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(b.k_cache.view(torch.uint8), kc.view(torch.uint8))
+    assert torch.equal(b.v_cache.view(torch.uint8), vc.view(torch.uint8))

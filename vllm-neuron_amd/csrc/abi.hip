@@ -179,6 +179,11 @@ static int validate_decode(const mia_decode_args *a) {
                 MIA_ERR_VALUE,
                 "decode: active-row quantisation needs an fp8 cache and both scales");
   }
+  if (a->write_slots) {
+    MIA_REQUIRE(a->write_slot_dtype == MIA_DTYPE_I32 || a->write_slot_dtype == MIA_DTYPE_I64 ||
+                    a->write_slot_dtype == MIA_DTYPE_U32,
+                MIA_ERR_VALUE, "decode: write slots must be i32, i64 or u32");
+  }
   return MIA_OK;
 }
 

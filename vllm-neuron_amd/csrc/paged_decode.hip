@@ -548,7 +548,6 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeKParams p) {
 // ---------------------------------------------------------------------------
 struct CombineParams {
   DecodeKParams k;  // shared geometry (col0 unused)
-  int D;
   const uint16_t *k_new;
   const uint16_t *v_new;
   int64_t kn_b, kn_s, kn_h;
@@ -557,132 +556,196 @@ struct CombineParams {
   const float *sink;         // [Hq] or null
   const float *v_deq;
   float act_scale_log2;      // softmax_scale * log2(e)
-  int fp8;                   // round-trip active rows through e4m3fn
-  int quant_mode;
+  int fp8;                   // cache partials hold v * 2^-8
+  int quant_mode;            // round trip of the active rows (fp8 cache)
   const float *k_quant;
   const float *v_quant;
   int quant_per_head;
   uint16_t *out;
   int64_t os_b, os_s, os_h;
+  // fused cache update of the active rows (stage 8), optional
+  const void *wslots;
+  int wslot_dtype;
+  int cache_dtype;
+  uint8_t *k_cache_w;
+  uint8_t *v_cache_w;
 };
 
-constexpr int kMaxCols = 64;
 constexpr int kMaxAct = 16;
+constexpr int kSplitBatch = 16;
 
-MIA_DEV float active_value(const CombineParams &c, const uint16_t *base,
-                           int64_t idx, int h, const float *qscale) {
-  float x = bf16_bits_to_f32(base[idx]);
+MIA_DEV float quant_roundtrip(const CombineParams &c, float x, int h, const float *qscale) {
   if (c.quant_mode == MIA_QUANT_NONE) return x;
   const float s = qscale[c.quant_per_head ? h : 0];
   return e4m3fn_bits_to_f32(quantize_e4m3fn(x, s, c.quant_mode));
 }
 
-__global__ __launch_bounds__(256) void decode_combine_kernel(CombineParams c) {
+// One wave per (column, kv head, batch row): merges the split partials of
+// the row (online, kSplitBatch at a time, all loads of a batch in flight
+// together), adds the active keys and the sink, normalises, writes bf16.
+// The wave of column 0 also writes the active rows into the cache when
+// write slots are given (after every split kernel has read the cache).
+template <int D>
+__global__ __launch_bounds__(64) void decode_combine_kernel(CombineParams c) {
+  constexpr int DPL = D / 64;  // d values per lane
   const DecodeKParams &p = c.k;
-  const int h = blockIdx.x;
-  const int b = blockIdx.y;
-  const int D = c.D;
-  const int NC = p.nc_tot;
+  const int col = blockIdx.x;
+  const int h = blockIdx.y;
+  const int b = blockIdx.z;
+  const int lane = threadIdx.x;
   const int S = p.S;
-  const int wave = threadIdx.x >> 6;
-  const int lane = threadIdx.x & 63;
+  const int NC = p.nc_tot;
+  const int s_q = col / p.G;
+  const int hq = h * p.G + col % p.G;
 
-  __shared__ float act[kMaxCols][kMaxAct];
-  __shared__ float colM[kMaxCols];
-  __shared__ float colL[kMaxCols];
-
-  const RowInfo ri = row_info(p.pos, p.start, p.mask_mode, S, p.s_ctx, b);
-  int sp0 = 0, sp1 = 0;
-  if (ri.lo < ri.hi) {
-    sp0 = ri.lo / p.split_tokens;
-    sp1 = (ri.hi + p.split_tokens - 1) / p.split_tokens;
-  }
-  const float kdeq = p.k_deq ? p.k_deq[h] : 1.0f;
-  const float ascale = c.act_scale_log2 * kdeq;
-  const int64_t row0 = ((int64_t)b * p.Hkv + h) * p.num_splits;
-
-  // 1) active-token scores: one wave per (column, key) pair, lanes over d.
-  for (int pair = wave; pair < NC * S; pair += kWaves) {
-    const int col = pair / S;
-    const int k = pair % S;
-    const int s_q = col / p.G;
-    const int hq = h * p.G + col % p.G;
-    bool ok;
-    if (p.mask_mode == 1) {
-      const int64_t lin = seq_to_linear((int64_t)p.s_ctx - S + k, p.mask_bl);
-      ok = p.full_mask[((lin * p.B + b) * p.Hq + hq) * S + s_q] != 0.f;
-    } else if (c.active_mask) {
-      ok = c.active_mask[(((int64_t)k * p.B + b) * p.Hq + hq) * S + s_q] != 0.f;
-    } else {
-      ok = k <= s_q;
-    }
-    const uint16_t *qp = p.q + b * p.qs_b + (int64_t)s_q * p.qs_s + hq * p.qs_h;
-    const int64_t kb = b * c.kn_b + (int64_t)k * c.kn_s + (int64_t)h * c.kn_h;
-    float dot = 0.f;
-    for (int d = lane; d < D; d += 64)
-      dot = fmaf(bf16_bits_to_f32(qp[d]),
-                 active_value(c, c.k_new, kb + d, h, c.k_quant), dot);
+  // ---- independent loads: query, active rows, scales, positions
+  float q[DPL];
+  const uint16_t *qp = p.q + b * p.qs_b + (int64_t)s_q * p.qs_s + hq * p.qs_h;
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) dot = wave_sum_xor(dot, m);
-    if (lane == 0) act[col][k] = ok ? dot * ascale : -INFINITY;
-  }
-  __syncthreads();
-
-  // 2) per-column max and denominator: one wave per column, lanes over splits.
-  for (int col = wave; col < NC; col += kWaves) {
-    const int hq = h * p.G + col % p.G;
-    const float sink2 = c.sink ? c.sink[hq] * kLog2e : -INFINITY;
-    float M = -INFINITY;
-    for (int sp = sp0 + lane; sp < sp1; sp += 64)
-      M = fmaxf(M, p.ws_ml[((row0 + sp) * NC + col) * 2]);
+  for (int j = 0; j < DPL; ++j) q[j] = bf16_bits_to_f32(qp[lane + 64 * j]);
+  uint32_t kraw[kMaxAct][DPL], vraw[kMaxAct][DPL];
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) M = wave_max_xor(M, m);
-    M = fmaxf(M, sink2);
-    for (int k = 0; k < S; ++k) M = fmaxf(M, act[col][k]);
-    const float Mu = (M == -INFINITY) ? 0.f : M;
-    float L = 0.f;
-    for (int sp = sp0 + lane; sp < sp1; sp += 64) {
-      const int64_t r = (row0 + sp) * NC + col;
-      L += p.ws_ml[r * 2 + 1] * __builtin_amdgcn_exp2f(p.ws_ml[r * 2] - Mu);
-    }
+  for (int k = 0; k < kMaxAct; ++k) {
+    if (k < S) {
+      const int64_t kb = b * c.kn_b + (int64_t)k * c.kn_s + (int64_t)h * c.kn_h;
+      const int64_t vb = b * c.vn_b + (int64_t)k * c.vn_s + (int64_t)h * c.vn_h;
 #pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) L = wave_sum_xor(L, m);
-    if (lane == 0) {
-      L += __builtin_amdgcn_exp2f(sink2 - Mu);
-      for (int k = 0; k < S; ++k) L += __builtin_amdgcn_exp2f(act[col][k] - Mu);
-      colM[col] = Mu;
-      colL[col] = L;
-    }
-  }
-  __syncthreads();
-
-  // 3) output: one thread per (column, d); split loads are independent and
-  // unrolled so they are in flight together.
-  const float vdeq = (c.v_deq ? c.v_deq[h] : 1.0f);
-  const float vpart_scale = c.fp8 ? 256.0f : 1.0f;  // fp8 partials hold v*2^-8
-  for (int idx = threadIdx.x; idx < NC * D; idx += blockDim.x) {
-    const int col = idx / D;
-    const int d = idx % D;
-    const int s_q = col / p.G;
-    const int hq = h * p.G + col % p.G;
-    const float Mu = colM[col];
-    float acc = 0.f;
-#pragma unroll 8
-    for (int sp = sp0; sp < sp1; ++sp) {
-      const int64_t r = (row0 + sp) * NC + col;
-      acc += p.ws_o[r * D + d] * __builtin_amdgcn_exp2f(p.ws_ml[r * 2] - Mu);
-    }
-    acc *= vpart_scale;
-    for (int k = 0; k < S; ++k) {
-      const float pk = __builtin_amdgcn_exp2f(act[col][k] - Mu);
-      if (pk != 0.f) {
-        const int64_t vb = b * c.vn_b + (int64_t)k * c.vn_s + (int64_t)h * c.vn_h;
-        acc += pk * active_value(c, c.v_new, vb + d, h, c.v_quant);
+      for (int j = 0; j < DPL; ++j) {
+        kraw[k][j] = c.k_new[kb + lane + 64 * j];
+        vraw[k][j] = c.v_new[vb + lane + 64 * j];
       }
     }
-    const float outv = acc / colL[col] * vdeq;
-    c.out[b * c.os_b + (int64_t)s_q * c.os_s + hq * c.os_h + d] =
-        (uint16_t)f32_to_bf16_bits(outv);
+  }
+  const float kdeq = p.k_deq ? p.k_deq[h] : 1.0f;
+  const float vdeq = c.v_deq ? c.v_deq[h] : 1.0f;
+  const float sink2 = c.sink ? c.sink[hq] * kLog2e : -INFINITY;
+  const RowInfo ri = row_info(p.pos, p.start, p.mask_mode, S, p.s_ctx, b);
+
+  // ---- split partials, merged online
+  float M = -INFINITY, L = 0.f, acc[DPL];
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
+  if (ri.lo < ri.hi) {
+    const int sp0 = ri.lo / p.split_tokens;
+    const int sp1 = (ri.hi + p.split_tokens - 1) / p.split_tokens;
+    const int64_t row0 = ((int64_t)b * p.Hkv + h) * p.num_splits;
+    for (int s0 = sp0; s0 < sp1; s0 += kSplitBatch) {
+      float ms[kSplitBatch], ls[kSplitBatch], os[kSplitBatch][DPL];
+#pragma unroll
+      for (int i = 0; i < kSplitBatch; ++i) {
+        const int sp = min(s0 + i, sp1 - 1);  // in bounds; extras masked below
+        const int64_t r = (row0 + sp) * NC + col;
+        ms[i] = p.ws_ml[r * 2];
+        ls[i] = p.ws_ml[r * 2 + 1];
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) os[i][j] = p.ws_o[r * D + lane + 64 * j];
+      }
+      float bm = M;
+#pragma unroll
+      for (int i = 0; i < kSplitBatch; ++i)
+        if (s0 + i < sp1) bm = fmaxf(bm, ms[i]);
+      const float bmu = (bm == -INFINITY) ? 0.f : bm;
+      const float f = __builtin_amdgcn_exp2f(M - bmu);
+      L *= f;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) acc[j] *= f;
+#pragma unroll
+      for (int i = 0; i < kSplitBatch; ++i) {
+        if (s0 + i < sp1) {
+          const float w = __builtin_amdgcn_exp2f(ms[i] - bmu);
+          L += ls[i] * w;
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) acc[j] += os[i][j] * w;
+        }
+      }
+      M = bm;
+    }
+  }
+  const float vpart_scale = c.fp8 ? 256.0f : 1.0f;  // fp8 partials hold v*2^-8
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) acc[j] *= vpart_scale;
+
+  // ---- active keys (the last S slots of the gathered context)
+  const float ascale = c.act_scale_log2 * kdeq;
+  float sk[kMaxAct];
+#pragma unroll
+  for (int k = 0; k < kMaxAct; ++k) {
+    sk[k] = -INFINITY;
+    if (k < S) {
+      bool ok;
+      if (p.mask_mode == 1) {
+        const int64_t lin = seq_to_linear((int64_t)p.s_ctx - S + k, p.mask_bl);
+        ok = p.full_mask[((lin * p.B + b) * p.Hq + hq) * S + s_q] != 0.f;
+      } else if (c.active_mask) {
+        ok = c.active_mask[(((int64_t)k * p.B + b) * p.Hq + hq) * S + s_q] != 0.f;
+      } else {
+        ok = k <= s_q;
+      }
+      float dot = 0.f;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j)
+        dot = fmaf(q[j], quant_roundtrip(c, bf16_bits_to_f32(kraw[k][j]), h, c.k_quant), dot);
+#pragma unroll
+      for (int m = 32; m >= 1; m >>= 1) dot = wave_sum_xor(dot, m);
+      if (ok) sk[k] = dot * ascale;
+    }
+  }
+  float bm = fmaxf(M, sink2);
+#pragma unroll
+  for (int k = 0; k < kMaxAct; ++k) bm = fmaxf(bm, sk[k]);
+  const float bmu = (bm == -INFINITY) ? 0.f : bm;
+  const float f = __builtin_amdgcn_exp2f(M - bmu);
+  L = L * f + __builtin_amdgcn_exp2f(sink2 - bmu);
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) acc[j] *= f;
+#pragma unroll
+  for (int k = 0; k < kMaxAct; ++k) {
+    if (k < S) {
+      const float pk = __builtin_amdgcn_exp2f(sk[k] - bmu);
+      L += pk;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j)
+        acc[j] += pk * quant_roundtrip(c, bf16_bits_to_f32(vraw[k][j]), h, c.v_quant);
+    }
+  }
+  uint16_t *op = c.out + b * c.os_b + (int64_t)s_q * c.os_s + hq * c.os_h;
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) op[lane + 64 * j] = (uint16_t)f32_to_bf16_bits(acc[j] / L * vdeq);
+
+  // ---- fused cache update of the active rows
+  if (c.wslots && col == 0) {
+    const int64_t max_slot = (int64_t)p.nb * p.bs;
+#pragma unroll
+    for (int k = 0; k < kMaxAct; ++k) {
+      if (k >= S) break;
+      int64_t slot;
+      const int64_t si = (int64_t)b * S + k;
+      if (c.wslot_dtype == MIA_DTYPE_I64) slot = ((const int64_t *)c.wslots)[si];
+      else if (c.wslot_dtype == MIA_DTYPE_U32) slot = ((const uint32_t *)c.wslots)[si];
+      else slot = ((const int32_t *)c.wslots)[si];
+      if (slot < 0 || slot >= max_slot) continue;  // sentinel: skipped
+      const int64_t blk = slot / p.bs, off = slot % p.bs;
+      const int64_t kd = blk * p.kc_blk + h * p.kc_h + off * p.kc_t;
+      const int64_t vd = blk * p.vc_blk + h * p.vc_h + off * p.vc_t;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        const int e = lane + 64 * j;
+        if (c.cache_dtype == MIA_DTYPE_FP8_E4M3FN) {
+          const float ks = c.k_quant ? c.k_quant[c.quant_per_head ? h : 0] : 1.f;
+          const float vs = c.v_quant ? c.v_quant[c.quant_per_head ? h : 0] : 1.f;
+          const float kx = bf16_bits_to_f32(kraw[k][j]), vx = bf16_bits_to_f32(vraw[k][j]);
+          c.k_cache_w[kd + e] = (uint8_t)(c.quant_mode == MIA_QUANT_NONE
+                                              ? f32_to_e4m3fn_bits(kx)
+                                              : quantize_e4m3fn(kx, ks, c.quant_mode));
+          c.v_cache_w[vd + e] = (uint8_t)(c.quant_mode == MIA_QUANT_NONE
+                                              ? f32_to_e4m3fn_bits(vx)
+                                              : quantize_e4m3fn(vx, vs, c.quant_mode));
+        } else {
+          ((uint16_t *)c.k_cache_w)[kd + e] = (uint16_t)kraw[k][j];
+          ((uint16_t *)c.v_cache_w)[vd + e] = (uint16_t)vraw[k][j];
+        }
+      }
+    }
   }
 }
 
@@ -710,7 +773,16 @@ DecodePlan plan_decode(const mia_decode_args &a) {
   // streamed by one wave.  The chunk is a shape-only choice (graph
   // capturable, no host sync), a multiple of the 32-token tile whose block
   // ids fit in one wave register.
-  int st = a.split_tokens > 0 ? a.split_tokens : kDefaultChunk;
+  int st = a.split_tokens;
+  if (st <= 0) {
+    // about 8 worst-case items per streaming wave, 32..256 tokens each:
+    // small problems get short items so that every wave has work.
+    const int64_t waves = 2 * (int64_t)device_cu_count() * kWaves;
+    const int64_t tokens = (int64_t)a.batch * a.num_kv_heads * s_ctx;
+    const int64_t want = tokens / (8 * waves);
+    st = kTile;
+    while (st < want && st < kDefaultChunk) st <<= 1;
+  }
   st = ((st + kTile - 1) / kTile) * kTile;
   const int st_cap = std::min(kMaxSplitTokens, (63 * a.block_size / kTile) * kTile);
   if (st > st_cap) st = st_cap;
@@ -808,7 +880,6 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
   kp.col0 = 0;
   CombineParams cp;
   cp.k = kp;
-  cp.D = a.head_dim;
   cp.k_new = (const uint16_t *)a.k_new;
   cp.v_new = (const uint16_t *)a.v_new;
   cp.kn_b = a.k_new_stride[0];
@@ -830,9 +901,16 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
   cp.os_b = a.out_stride[0];
   cp.os_s = a.out_stride[1];
   cp.os_h = a.out_stride[2];
-  hipLaunchKernelGGL(decode_combine_kernel,
-                     dim3((unsigned)a.num_kv_heads, (unsigned)a.batch),
-                     dim3(256), 0, s, cp);
+  cp.wslots = a.write_slots;
+  cp.wslot_dtype = a.write_slot_dtype;
+  cp.cache_dtype = a.cache_dtype;
+  cp.k_cache_w = (uint8_t *)a.k_cache;
+  cp.v_cache_w = (uint8_t *)a.v_cache;
+  const dim3 cgrid((unsigned)pl.ncols, (unsigned)a.num_kv_heads, (unsigned)a.batch);
+  if (a.head_dim == 128)
+    hipLaunchKernelGGL(decode_combine_kernel<128>, cgrid, dim3(64), 0, s, cp);
+  else
+    hipLaunchKernelGGL(decode_combine_kernel<64>, cgrid, dim3(64), 0, s, cp);
   return check_hip(hipGetLastError(), "decode combine launch");
 }
 

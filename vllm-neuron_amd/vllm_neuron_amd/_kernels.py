@@ -244,9 +244,14 @@ def paged_decode(
     workspace: Optional[torch.Tensor] = None,
     split_tokens: int = 0,
     split_events: Optional[tuple] = None,
+    write_slots: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Attention of ``q [B, S, Hq, d]`` over the paged prior context plus the
     active rows ``k_new/v_new [B, S, Hkv, d]``; returns ``[B, S, Hq, d]`` bf16.
+
+    ``write_slots [B, S]`` (int32/int64) fuses the cache update: the active
+    rows are written to those slots after attention has read the cache;
+    slots outside the pool are skipped.
     """
     dev = N.require_gpu(q, k_new, v_new, k_cache, v_cache, block_table)
     if block_table.dtype != torch.int32:
@@ -343,6 +348,15 @@ def paged_decode(
         # kernels alone
         a.split_event_begin = split_events[0].cuda_event
         a.split_event_end = split_events[1].cuda_event
+    if write_slots is not None:
+        if write_slots.numel() != B * S:
+            raise ValueError(f"write_slots must hold B*S = {B * S} slots")
+        write_slots = write_slots.reshape(-1).to(dev)
+        if write_slots.dtype not in (torch.int32, torch.int64):
+            write_slots = write_slots.to(torch.int64)
+        write_slots = write_slots.contiguous()
+        a.write_slots = write_slots.data_ptr()
+        a.write_slot_dtype = N.mia_dtype(write_slots.dtype)
     L = N.lib()
     need = L.mia_decode_workspace_bytes(ctypes.byref(a))
     if need == 0:

@@ -321,7 +321,11 @@ def attention_decode(
         q = _torch_rms_norm_heads(q, rmsnorm_QK_post_rope_eps, rmsnorm_QK_post_rope_W_Q)
         k = _torch_rms_norm_heads(k, rmsnorm_QK_post_rope_eps, rmsnorm_QK_post_rope_W_K)
 
-    # ---- stage 7: attention core (HIP)
+    # ---- stage 7 (+ stage 8 fused when the K layout is unpacked): HIP
+    fuse_write = update_cache and not fp8_packed
+    if update_cache:
+        assert kv_cache_update_idx is not None, (
+            "kv_cache_update_idx must be provided when update_cache=True")
     attn = paged_decode_core(
         q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
         K_cache, V_cache, active_blocks_table,
@@ -331,16 +335,16 @@ def attention_decode(
         softmax_scale=softmax_scale if softmax_scale is not None else d_head ** -0.5,
         k_scale=k_scale, v_scale=v_scale, fp8_packed=fp8_packed,
         k_dequant_scale=k_dequant_scale, v_dequant_scale=v_dequant_scale,
+        write_slots=kv_cache_update_idx if fuse_write else None,
     )  # [B, S, Hq, d]
 
-    # ---- stage 8: KV cache update (HIP)
+    # ---- stage 8: KV cache update (HIP; separate scatter for packed K)
     k_rows = k.transpose(1, 2).reshape(B * S_tkg, kv_heads, d_head)
     v_rows = v.transpose(1, 2).reshape(B * S_tkg, kv_heads, d_head)
     if update_cache:
-        assert kv_cache_update_idx is not None, (
-            "kv_cache_update_idx must be provided when update_cache=True")
-        _write_rows(k_rows, v_rows, kv_cache_update_idx, K_cache, V_cache,
-                    k_scale, v_scale, kv_heads, fp8_packed)
+        if not fuse_write:
+            _write_rows(k_rows, v_rows, kv_cache_update_idx, K_cache, V_cache,
+                        k_scale, v_scale, kv_heads, fp8_packed)
         K_out = V_out = None
     else:
         K_out, V_out = _new_kv_for_return(k, v, k_rows, v_rows, K_cache, k_scale,
@@ -381,11 +385,13 @@ def paged_decode_core(
     workspace: Optional[Tensor] = None,
     split_tokens: int = 0,
     split_events: Optional[tuple] = None,
+    write_slots: Optional[Tensor] = None,
 ) -> Tensor:
     """Attention core of stages 7a-7g: ``q [B, S, Hq, d]`` attends to the
     paged prior context and the active rows ``k_new/v_new [B, S, Hkv, d]``
     (placed at the last S slots of the context, as the reference does).
-    Returns ``[B, S, Hq, d]`` bf16."""
+    ``write_slots [B*S]`` fuses stage 8 (the cache update) into the same
+    launch sequence.  Returns ``[B, S, Hq, d]`` bf16."""
     B, S, Hq, d = q.shape
     kv_heads = k_new.shape[2]
     fp8 = K_cache.dtype == torch.float8_e4m3fn
@@ -393,11 +399,14 @@ def paged_decode_core(
         raise NotImplementedError("k_scale/v_scale are only meaningful with an fp8 KV cache")
     if fp8 and V_cache.dtype != K_cache.dtype:
         raise ValueError("K and V caches must share a dtype")
+    if fp8_packed and write_slots is not None:
+        raise NotImplementedError("fused cache update needs the unpacked K layout")
     k_read = _unswizzle_packed_k(K_cache) if fp8_packed else K_cache
 
     kw = dict(softmax_scale=softmax_scale, sink=sink,
               k_dequant=k_dequant_scale, v_dequant=v_dequant_scale,
-              workspace=workspace, split_tokens=split_tokens, split_events=split_events)
+              workspace=workspace, split_tokens=split_tokens, split_events=split_events,
+              write_slots=write_slots)
     if k_scale is not None:
         kw["quant_mode"] = _quant_mode_for(k_new.dtype, k_scale)
         kw["k_quant"] = k_scale
