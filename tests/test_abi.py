@@ -1,0 +1,144 @@
+"""The C ABI on the CPU: the library loads without a GPU, exports every entry
+point declared in include/*.h, its argument structs have the layout the
+Python binding declares, and argument validation reports the documented
+error classes before anything reaches the device (no kernel is launched
+here: every call below fails validation).
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+from vllm_neuron_amd import _native as N
+
+ROOT = Path(__file__).resolve().parent.parent
+DECL = re.compile(r"^[A-Za-z_][\w\s\*]*?\b(mia_\w+)\s*\(", re.M)
+
+
+def _declared():
+    names = set()
+    for h in (ROOT / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names.update(DECL.findall(text))
+    return names
+
+
+def test_header_declares_the_documented_entry_points():
+    names = _declared()
+    for must in ("mia_abi_version", "mia_last_error", "mia_paged_decode", "mia_paged_prefill",
+                 "mia_kv_write", "mia_decode_workspace_bytes", "mia_decode_mask",
+                 "mia_gather_kv"):
+        assert must in names
+    assert names == set(N.EXPORTS), "binding export list out of date"
+
+
+def test_library_exports_every_declared_symbol():
+    L = N.lib()
+    for name in _declared():
+        assert hasattr(L, name), f"{name} declared in include/ but not exported"
+    assert L.mia_abi_version() == 1
+
+
+def test_struct_layout_matches_binding():
+    L = N.lib()   # lib() itself refuses a size mismatch; check explicitly too
+    for which, st in N.ARGS_STRUCTS.items():
+        assert L.mia_args_size(which) == ctypes.sizeof(st), st.__name__
+    assert L.mia_args_size(99) == 0
+
+
+def _decode_args(**over):
+    a = N.DecodeArgs()
+    fake = 0x10000  # never dereferenced: validation fails first
+    for f in ("q", "k_new", "v_new", "k_cache", "v_cache", "block_table", "out", "pos_ids"):
+        setattr(a, f, fake)
+    a.q_stride = (ctypes.c_int64 * 4)(4096, 4096, 128, 1)
+    a.k_new_stride = (ctypes.c_int64 * 4)(1024, 1024, 128, 1)
+    a.v_new_stride = (ctypes.c_int64 * 4)(1024, 1024, 128, 1)
+    a.k_cache_stride = (ctypes.c_int64 * 5)(32768, 4096, 128, 1, 0)
+    a.v_cache_stride = (ctypes.c_int64 * 4)(32768, 4096, 128, 1)
+    a.cache_dtype = N.DTYPE_BF16
+    a.num_blocks, a.block_size, a.blocks_per_seq = 100, 32, 8
+    a.batch, a.s_active, a.num_q_heads, a.num_kv_heads, a.head_dim = 2, 1, 32, 8, 128
+    a.out_dtype = N.DTYPE_BF16
+    a.out_stride = (ctypes.c_int64 * 4)(4096, 4096, 128, 1)
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("over,err,text", [
+    (dict(head_dim=96), NotImplementedError, "head_dim"),
+    (dict(num_q_heads=30), ValueError, "GQA"),
+    (dict(block_size=8), NotImplementedError, "block_size"),
+    (dict(s_active=17), NotImplementedError, "active tokens"),
+    (dict(num_q_heads=128, num_kv_heads=1), NotImplementedError, "query columns"),
+    (dict(batch=1025), NotImplementedError, "1024"),
+    (dict(k_cache=0x10004), ValueError, "aligned"),
+    (dict(cache_dtype=N.DTYPE_F32), NotImplementedError, "cache dtype"),
+    (dict(pos_ids=None), ValueError, "pos_ids"),
+    (dict(quant_mode=1), ValueError, "quantisation"),
+    (dict(write_slots=0x10000, write_slot_dtype=N.DTYPE_F32), ValueError, "write slots"),
+    (dict(blocks_per_seq=0), ValueError, "empty"),
+])
+def test_decode_validation(over, err, text):
+    a = _decode_args(**over)
+    L = N.lib()
+    assert L.mia_decode_workspace_bytes(ctypes.byref(a)) == 0
+    rc = L.mia_paged_decode(ctypes.byref(a), None)
+    with pytest.raises(err, match=text):
+        N.check(rc, "paged_decode")
+
+
+def test_null_args_are_value_errors():
+    L = N.lib()
+    for fn in (L.mia_paged_decode, L.mia_paged_prefill, L.mia_kv_write, L.mia_gather_kv,
+               L.mia_decode_mask, L.mia_slot_mapping, L.mia_swa_trim, L.mia_packed_k_convert,
+               L.mia_scatter_rows):
+        rc = fn(None, None)
+        assert rc == N.MIA_ERR_VALUE, fn.__name__
+        assert L.mia_last_error()  # a message was recorded
+    assert L.mia_slot_mapping_host(None) == N.MIA_ERR_VALUE
+
+
+def test_kv_write_validation():
+    L = N.lib()
+    a = N.KvWriteArgs()
+    a.k_src = a.slots = a.k_cache = 0x10000
+    a.num_tokens = 4
+    a.src_dtype = N.DTYPE_BF16
+    a.slot_dtype = N.DTYPE_F32
+    a.cache_dtype = N.DTYPE_BF16
+    a.num_blocks = a.block_size = a.num_kv_heads = a.head_dim = 8
+    with pytest.raises(ValueError, match="slot dtype"):
+        N.check(L.mia_kv_write(ctypes.byref(a), None), "kv_write")
+    a.slot_dtype = N.DTYPE_I64
+    a.quant_mode = 1
+    with pytest.raises(ValueError, match="fp8 cache"):
+        N.check(L.mia_kv_write(ctypes.byref(a), None), "kv_write")
+    a.num_tokens = 0  # nothing to do: succeeds without touching the device
+    assert L.mia_kv_write(ctypes.byref(a), None) == N.MIA_OK
+
+
+def test_error_state_is_cleared_by_the_next_call():
+    L = N.lib()
+    L.mia_paged_decode(None, None)
+    assert L.mia_last_error()
+    a = N.KvWriteArgs()
+    assert L.mia_kv_write(ctypes.byref(a), None) == N.MIA_OK  # num_tokens == 0
+    assert L.mia_last_error() == b""
+
+
+def test_host_slot_mapping_through_abi():
+    bt = np.array([[10, 15, 0, 0]], np.int32)
+    pos = np.array([62, 63, 64, 65], np.int64)
+    req = np.zeros(4, np.int64)
+    out = np.zeros(4, np.int64)
+    a = N.SlotMappingArgs()
+    a.block_table, a.bt_row_stride, a.max_blocks_per_req, a.block_size = bt.ctypes.data, 4, 4, 64
+    a.positions, a.req_indices, a.num_tokens = pos.ctypes.data, req.ctypes.data, 4
+    a.cp_world_size, a.cp_rank, a.cp_interleave = 1, 0, 1
+    a.slot_mapping = out.ctypes.data
+    assert N.lib().mia_slot_mapping_host(ctypes.byref(a)) == N.MIA_OK
+    assert out.tolist() == [702, 703, 960, 961]
