@@ -4,8 +4,9 @@
 Workload (N=1): Llama-3-8B-shaped paged decode — 32 q / 8 kv heads,
 head_dim 128, bf16, batch 64, contexts U[512, 8192], block_size 32, random
 non-contiguous block tables, N(0,1) inputs.  A step is one decode attention
-pass over the batch: the split-K attention kernels plus the KV-cache write
-of the 64 new tokens, inputs resident in HBM.
+pass over the batch: the split-K attention kernel plus the combine kernel,
+which also writes the 64 new tokens' K/V rows into the cache; inputs are
+resident in HBM.
 
 The same line carries
   * ``roofline`` for the dominant kernel (the split-K decode kernel, HBM
@@ -39,24 +40,19 @@ METRIC = "decode-attn KV GB/s (% of HBM peak) + prefill TFLOP/s at 8B shape, 1 G
 def _decode_step_fn(b, dev):
     import torch
 
-    from vllm_neuron_amd import _kernels as K
     from vllm_neuron_amd.functional.attention.attention_decode import paged_decode_core
 
     cfg = b.cfg
     S_ctx = b.block_table.shape[1] * cfg.block_size
-    out = torch.empty_like(b.q)
     # workspace sized once (the library never allocates)
     ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
-    k_rows = b.k_new.reshape(cfg.batch, cfg.kv_heads, cfg.head_dim)
-    v_rows = b.v_new.reshape(cfg.batch, cfg.kv_heads, cfg.head_dim)
+    slots = b.slots.reshape(-1).contiguous()
 
     def step(events=None):
-        paged_decode_core(b.q, b.k_new, b.v_new, b.k_cache, b.v_cache, b.block_table,
-                          block_len=cfg.block_size, S_ctx=S_ctx, pos_ids=b.pos,
-                          softmax_scale=cfg.head_dim ** -0.5, workspace=ws,
-                          split_events=events)
-        K.kv_write(k_rows, v_rows, b.slots, b.k_cache, b.v_cache)
-        return out
+        return paged_decode_core(b.q, b.k_new, b.v_new, b.k_cache, b.v_cache, b.block_table,
+                                 block_len=cfg.block_size, S_ctx=S_ctx, pos_ids=b.pos,
+                                 softmax_scale=cfg.head_dim ** -0.5, workspace=ws,
+                                 split_events=events, write_slots=slots)
 
     return step
 
@@ -175,6 +171,21 @@ def cpu_baseline(gpu_batch, rows=16):
     }
 
 
+def _measured_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of ``kernel`` on ``workload`` as measured with
+    rocprofv3 FETCH_SIZE / WRITE_SIZE counters (scaled by the same counters
+    read on a plain copy of known size), from profiles/*_traffic.json;
+    None when no such measurement is committed."""
+    for f in sorted((ROOT / "profiles").glob("*_traffic.json")):
+        try:
+            rec = json.loads(f.read_text())
+        except (OSError, ValueError):
+            continue
+        if rec.get("kernel") == kernel and rec.get("workload") == workload:
+            return rec.get("hbm_bytes_per_launch")
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -183,6 +194,9 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=16,
                     help="batch rows of the decode batch timed on the CPU")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="first run a plain device-to-device copy of this many MiB three "
+                         "times (the reference kernel for scaling HBM byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -195,6 +209,13 @@ def main() -> int:
     from vllm_neuron_amd import _native
 
     _native.lib()
+    if args.copy_mib > 0:
+        src = torch.ones(args.copy_mib << 20, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     dec = bench_decode(dev, args.steps, args.warmup)
     pre = bench_prefill(dev, max(5, args.steps // 2), max(2, args.warmup // 2))
     cfg = dec["cfg"]
@@ -222,13 +243,14 @@ def main() -> int:
             "hbm_frac_of_step": round(value / HBM_PEAK_GBS, 4),
         },
         "roofline": {
-            "kernel": "decode_split_kernel<128,4,bf16>",
+            "kernel": "decode_split_kernel<128, 4, false>",
             "bound": "hbm",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": _measured_traffic("decode_split_kernel<128, 4, false>",
+                                         "llama3_8b_paged_decode_b64_ctx512-8192"),
             "avg_launch_us": round(dec["split_avg_ms"] * 1e3, 2),
             "algorithmic_bytes": dec["split_bytes"],
         },
