@@ -1,36 +1,45 @@
 // paged_decode.hip — split-K flash decoding over a block-table KV cache for
 // gfx950 (wave64, MFMA, 160 KB LDS).
 //
-// Work decomposition
-//   grid  = (num_splits, Hkv, B) per column group; 256 threads = 4 waves.
-//   A workgroup owns one (batch row b, kv head h, split) and every query
-//   column of that GQA group: column c = s * G + g (query token s, head
-//   g of the group), up to 16 columns per launch.  K/V bytes of a split are
-//   read from HBM exactly once and shared by all G*S_tkg queries.
-//   Each wave takes 64-token tiles of the split in turn.
+// Work decomposition (split kernel)
+//   The prior context of batch row b, kv head h is cut into chunks of
+//   `split_tokens` tokens; a work item is one (b, h, chunk) that overlaps
+//   the row's attended range.  The grid is persistent (about 2 workgroups
+//   of 4 waves per CU); each wave streams items blockIdx*4+wave,
+//   +gridDim*4, ... independently of the other waves.  An item covers every
+//   query column of its GQA group (column = query token s x head g, up to
+//   16 per launch), so each K/V byte is read from HBM once.
+//   Every workgroup first computes each row's attended range and the prefix
+//   sum of items in LDS (rows <= 1024); a wave maps its item id to
+//   (b, h, chunk) by binary search.
 //
-// Per 64-token tile and wave
-//   K  : 4 sub-tiles of 16 tokens loaded straight into MFMA A-operand
-//        registers (lane = token row, 16 B = 8 consecutive d per lane; a
-//        load instruction covers 16 rows x 64 contiguous bytes).
+// Per 32-token tile and wave
+//   K  : 2 sub-tiles of 16 tokens loaded straight into MFMA A-operand
+//        registers (lane = token row, 16 B = 8 consecutive d per lane).
 //   QK : v_mfma_f32_16x16x32_bf16, A = K [16 tok x 32 d], B = Q^T [32 d x
 //        16 columns]; D/32 k-steps.  Result lane l holds tokens
 //        4*(l/16)+i, column l%16.
 //   softmax: masked scores, tile max via xor-shuffles over 16/32 lanes,
 //        online rescale (exp2 domain), per-lane partial row sums.
 //   PV : on the vector ALU in fp32: lane = (token lane, 8-wide d slice),
-//        V rows loaded 16 B per lane (an instruction covers whole 256-byte
-//        rows), probabilities exchanged through LDS.
-//   Block-table lookups are wave-uniform (block_size % 16 == 0) and go
-//   through the scalar cache.
-// End of split: xor-reduce partial sums, merge the 4 waves through LDS and
-// write (m, l, o[D]) per column to the workspace.
+//        V rows loaded 16 B per lane, probabilities exchanged through LDS.
+//   The next tile's K (V) loads are issued right after QK (PV) consumed the
+//   registers, across item boundaries, so one tile of loads is always in
+//   flight; every load address is clamped into the item's attended range so
+//   no load is predicated (out-of-range rows are masked after the load).
+//   Physical block ids of an item are held one per lane and read with
+//   v_readlane (block_size % 16 == 0 keeps a 16-token group in one block).
+// End of item: xor-reduce partial sums and write (m, l, o[D]) per column to
+// the workspace.
 //
-// Combine kernel (grid = (Hkv, B)): merges the valid splits of a row, adds
-// the S_tkg active (new) keys — which the reference places at the last
-// S_tkg slots of the gathered context (attention_decode.py:957-982) — and
-// the optional sink logit (attention_decode.py:1019-1024), normalises and
-// writes bf16.
+// Combine kernel (one wave per (column, kv head, row)): merges the row's
+// split partials, adds the S_tkg active (new) keys — which the reference
+// places at the last S_tkg slots of the gathered context
+// (attention_decode.py:957-982) — and the optional sink logit
+// (attention_decode.py:1019-1024), normalises and writes bf16.  With write
+// slots given it also performs the cache update of the active rows
+// (attention_decode.py:1081-1150) after every split kernel has read the
+// cache.
 #include <algorithm>
 
 #include "mia_device.h"
@@ -383,8 +392,6 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeKParams p) {
   raw_t vr[VPL];
   issue_k(kr, cur, blk_cur, first_tile(cur));
   issue_v(vr, cur, blk_cur, first_tile(cur));
-  const float kdeq_all = 1.0f;
-  (void)kdeq_all;
 
   while (true) {
     const Item nxt = decode_item(item_id + n_workers, cur);
