@@ -224,6 +224,8 @@ int mia_paged_prefill(const mia_prefill_args *a, mia_stream_t stream) {
               "prefill: packed K is read through an unpacked view");
   MIA_REQUIRE(a->block_size > 0 && a->num_blocks > 0 && a->blocks_per_seq >= 0,
               MIA_ERR_VALUE, "prefill: bad cache geometry");
+  MIA_REQUIRE(a->block_size % 4 == 0, MIA_ERR_NOT_IMPLEMENTED,
+              "prefill: block_size must be a multiple of 4");
   MIA_REQUIRE(a->sliding_window >= 0, MIA_ERR_VALUE, "prefill: negative window");
   const int eb = a->cache_dtype == MIA_DTYPE_FP8_E4M3FN ? 1 : 2;
   const size_t vec = a->cache_dtype == MIA_DTYPE_FP8_E4M3FN ? 8 : 16;
