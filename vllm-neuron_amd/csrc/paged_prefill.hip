@@ -366,6 +366,335 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// bf16 cache, head_dim 128: K/V tiles streamed straight into LDS
+// ---------------------------------------------------------------------------
+// Same products and softmax as prefill_kernel, with 8 waves (256 GQA-packed
+// rows) per workgroup and the 64-key K and V tiles travelling HBM -> LDS
+// with global_load_lds_dwordx4 (no registers, no VALU) through a 3-stage
+// ring: tiles t+1 and t+2 are in flight while tile t is computed, one
+// barrier per tile.  The block ids of the workgroup's key range are staged
+// in LDS once, so no global load sits between two tiles' copies.
+// A DMA instruction writes 64 lanes x 16 B contiguously, i.e. 4 rows of
+// 256 B; each lane picks which 16-byte chunk of its row it fetches, which
+// stores the rows XOR-swizzled:
+//   K: LDS chunk s of row r holds chunk s ^ (r & 15)  -> the 32 lanes that
+//      read one chunk column of 32 rows hit 16 distinct chunk positions;
+//   V: LDS chunk s of row r holds chunk s ^ ((r & 3) << 2) -> conflict-free
+//      for the transposed reads below.
+// The V^T operand of O^T = V^T P^T is read with ds_read_b64_tr_b16: within
+// each 16-lane group, result lane k gets element k % 4 of the 8 bytes read
+// by lane 4j + k/4, j = 0..3.  Lane (group gi, k) therefore addresses key
+// row base + k/4 and the 4 d values starting at 4 * (k % 4) of its group's
+// 16 columns, and receives 4 consecutive keys of column d = lane % 32.
+constexpr int kDmaWaves = 8;
+constexpr int kDmaRows = kDmaWaves * kRowsW;  // 256 rows per workgroup
+constexpr int kDmaIds = 4096;                 // block ids staged in LDS
+
+template <int D>
+__global__ __launch_bounds__(512, 1) void prefill_dma_kernel(PrefillKParams p) {
+  static_assert(D == 128, "256-byte rows");
+  constexpr int KSTEPS = D / 16;
+  constexpr int DBLK = D / 32;
+  constexpr int ROWB = D * 2;          // bytes per K/V row
+  constexpr int TILEB = kKT * ROWB;    // bytes per K (or V) tile
+  constexpr int NJ = 16 / kDmaWaves;   // DMA instructions per thread per tile (K and V each)
+  typedef short s16x4_t __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+  typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
+  typedef __attribute__((address_space(3))) void lds_void_t;
+
+  // One __shared__ object per stage: the compiler then sees that a copy
+  // into one stage cannot alias the reads of another and does not wait for
+  // it before computing.
+  __shared__ int32_t ids_lds[kDmaIds];
+  __shared__ __attribute__((aligned(1024))) uint8_t k_lds0[TILEB];
+  __shared__ __attribute__((aligned(1024))) uint8_t k_lds1[TILEB];
+  __shared__ __attribute__((aligned(1024))) uint8_t k_lds2[TILEB];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_lds0[TILEB];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_lds1[TILEB];
+  __shared__ __attribute__((aligned(1024))) uint8_t v_lds2[TILEB];
+
+  const int seq = blockIdx.z;
+  const int h = blockIdx.y;
+  const int G = p.G;
+  const int q_begin = p.cu[seq];
+  const int S_q = p.cu[seq + 1] - q_begin;
+  const int rows_total = S_q * G;
+  const int row0 = blockIdx.x * kDmaRows;
+  if (row0 >= rows_total) return;
+  const int prior = p.prior[seq];
+  const int tid = threadIdx.x;
+  const int wave = readfirstlane(tid >> 6);
+  const int lane = tid & 63;
+  const int half = lane >> 5;
+  const int rl = lane & 31;
+  const int s_ctx = p.nblk * p.bs;
+
+  const int r = row0 + wave * kRowsW + rl;
+  const int pos_r = r / G;
+  const int g_r = r - pos_r * G;
+  const bool row_ok = r < rows_total && q_begin + pos_r < p.num_tokens;
+  const int hq = h * G + g_r;
+  const int r_hi = min(min(prior + pos_r + 1, prior + S_q), s_ctx);
+  const int r_lo = p.window > 0 ? prior + pos_r - p.window + 1 : 0;
+
+  const int pos_lo = row0 / G;
+  const int pos_hi = min(S_q - 1, (row0 + kDmaRows - 1) / G);
+  const int kmax = min(min(prior + pos_hi + 1, prior + S_q), s_ctx);
+  const int kmin = p.window > 0 ? max(0, prior + pos_lo - p.window + 1) : 0;
+  const int full_hi = min(min(prior + pos_lo + 1, prior + S_q), s_ctx);
+  const int full_lo = p.window > 0 ? prior + pos_hi - p.window + 1 : 0;
+  const bool any_key = kmax > kmin;
+  const int kt0 = (kmin / kKT) * kKT;
+  const int kt_last = kmax > kt0 ? ((kmax - 1) / kKT) * kKT : kt0;
+
+  bf16x8_t qf[KSTEPS];
+  {
+    const uint16_t *qp = p.q + (int64_t)(q_begin + (row_ok ? pos_r : 0)) * p.qs_t +
+                         (int64_t)(row_ok ? hq : 0) * p.qs_h;
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      u32x4_t w = {0u, 0u, 0u, 0u};
+      if (row_ok) w = *reinterpret_cast<const u32x4_t *>(qp + ks * 16 + half * 8);
+      qf[ks] = __builtin_bit_cast(bf16x8_t, w);
+    }
+    // wait for Q here, before the copy ring starts: a wait placed by the
+    // compiler inside the loop would also drain the in-flight copies
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) asm volatile("" ::"v"(qf[ks]));
+  }
+  const float scale2 = p.scale_log2 * (p.k_deq ? p.k_deq[h] : 1.0f);
+  asm volatile("" ::"v"(scale2));
+  const int64_t bt_row = (int64_t)seq * p.bt_s + (int64_t)h * p.bt_h;
+
+  // ---- block ids of blocks b_lo .. b_hi (clamped into the pool)
+  const int b_lo = (int)fdiv((uint32_t)kt0, p.bs_div);
+  const int b_hi = min((int)fdiv((uint32_t)(kt_last + kKT - 1), p.bs_div), p.nblk - 1);
+  if (any_key) {
+    for (int i = tid; i <= b_hi - b_lo; i += blockDim.x) {
+      int32_t v = p.bt[bt_row + (int64_t)(b_lo + i) * p.bt_j];
+      ids_lds[i] = v < 0 ? 0 : (v >= p.nb ? p.nb - 1 : v);
+    }
+  }
+  __syncthreads();
+
+  // ---- DMA: instruction j of wave w covers rows 4q .. 4q+3, q = 8j + w;
+  // lane -> row 4q + lane/16, LDS chunk lane % 16.  block_size % 16 == 0,
+  // so the 4 rows of an instruction share a block (a wave-uniform id).
+  // The offset of key kt + row inside its block is (kt % bs) + (row % bs)
+  // (kt % 64 == 0 and either bs divides 64 or 64 divides bs).
+  const int dma_r = lane >> 4;
+  const int dma_s = lane & 15;
+  const uint8_t *k_head = p.k_cache + (int64_t)h * p.kc_h * 2;
+  const uint8_t *v_head = p.v_cache + (int64_t)h * p.vc_h * 2;
+  int64_t k_lane[NJ], v_lane[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) {
+    const int row = 4 * (kDmaWaves * j + wave) + dma_r;
+    const int roff = row % p.bs;
+    k_lane[j] = (int64_t)roff * p.kc_t * 2 + ((dma_s ^ (row & 15)) << 4);
+    v_lane[j] = (int64_t)roff * p.vc_t * 2 + ((dma_s ^ ((row & 3) << 2)) << 4);
+  }
+  // One 16-byte-per-lane copy HBM -> LDS (global_load_lds_dwordx4): lane
+  // data lands at lds_dst + 16 * lane.  Issued through inline assembly so
+  // that the compiler, which cannot tell the stages of the ring apart, does
+  // not add waits before reads of other stages; the waits for these copies
+  // are the explicit s_waitcnt in `step` below.
+  // M0 (the LDS base of the copy) is saved and restored around it.
+  auto dma16 = [&](const uint8_t *src, uint8_t *lds_dst) {
+    const uint32_t m0 =
+        readfirstlane((int)(uint32_t)(uintptr_t)(lds_void_t *)lds_dst);
+    uint32_t saved;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "global_load_lds_dwordx4 %2, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "s"(m0), "v"(src)
+        : "memory");
+  };
+  auto issue_tile = [&](int kt, uint8_t *k_dst, uint8_t *v_dst) {
+    const int ktoff = kt - (int)fdiv((uint32_t)kt, p.bs_div) * p.bs;  // kt % bs
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int q = kDmaWaves * j + wave;
+      const int bi = min((int)fdiv((uint32_t)(kt + 4 * q), p.bs_div), p.nblk - 1) - b_lo;
+      const int32_t phys = readfirstlane(ids_lds[bi]);
+      const int64_t kb = ((int64_t)phys * p.kc_blk + (int64_t)ktoff * p.kc_t) * 2;
+      const int64_t vb = ((int64_t)phys * p.vc_blk + (int64_t)ktoff * p.vc_t) * 2;
+      dma16(k_head + kb + k_lane[j], k_dst + q * 1024);
+      dma16(v_head + vb + v_lane[j], v_dst + q * 1024);
+    }
+  };
+
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+  f32x16_t acc_o[DBLK];
+#pragma unroll
+  for (int i = 0; i < DBLK; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc_o[i][e] = 0.f;
+
+  // transposed-read lane constants (see above)
+  const int tr_k = lane & 15;
+  const int tr_col = ((lane >> 4) & 1) * 16 + 4 * (tr_k & 3);
+  const int tr_row = half * 4 + (tr_k >> 2);
+
+  auto compute_tile = [&](int kt, const uint8_t *k_src, const uint8_t *v_src) {
+    const lds_u8_t *kb_lds = (const lds_u8_t *)k_src;
+    const lds_u8_t *vb_lds = (const lds_u8_t *)v_src;
+    // ---- S^T = K . Q^T
+    f32x16_t sacc[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int row = kb * 32 + rl;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sacc[kb][e] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) {
+        const int c = ks * 2 + half;
+        const u32x4_t a =
+            *(const __attribute__((address_space(3))) u32x4_t *)(kb_lds + row * ROWB +
+                                                                  ((c ^ (row & 15)) << 4));
+        sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                           qf[ks], sacc[kb], 0, 0, 0);
+      }
+    }
+    // lane value e of block kb: key kt + kb*32 + (e/4)*8 + half*4 + e%4
+    const bool full = (kt + kKT <= full_hi) && (kt >= full_lo);
+    if (!full) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int key = kt + kb * 32 + (e >> 2) * 8 + half * 4 + (e & 3);
+          const bool ok = row_ok && key < r_hi && key >= r_lo;
+          sacc[kb][e] = ok ? sacc[kb][e] : -INFINITY;
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[kb][e]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    // Lazy rescaling: the running max only moves when the tile's max
+    // exceeds it by more than 8 (log2 units), so probabilities stay below
+    // 2^8 and the accumulators are rescaled only on such tiles.
+    const bool bump = mx * scale2 > m_run + 8.0f;
+    if (__builtin_amdgcn_ballot_w64(bump)) {
+      const float m_new = bump ? mx * scale2 : m_run;
+      const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int i = 0; i < DBLK; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc_o[i][e] *= alpha;
+    }
+    const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
+    float psum = 0.f;
+    uint32_t pk[2][8];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 16; e += 2) {
+        const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][e], scale2, -m_use));
+        const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][e + 1], scale2, -m_use));
+        psum += p0 + p1;
+        pk[kb][e >> 1] = pack2_bf16(p0, p1);
+      }
+    l_run += psum;
+
+    // ---- O^T += V^T . P^T
+#pragma unroll
+    for (int ks2 = 0; ks2 < 4; ++ks2) {
+      const int kb = ks2 >> 1, kh = ks2 & 1;
+      const u32x4_t bw = {pk[kb][kh * 4 + 0], pk[kb][kh * 4 + 1], pk[kb][kh * 4 + 2],
+                          pk[kb][kh * 4 + 3]};
+      const bf16x8_t bop = __builtin_bit_cast(bf16x8_t, bw);
+#pragma unroll
+      for (int db = 0; db < DBLK; ++db) {
+        s16x4_t t2[2];
+#pragma unroll
+        for (int rr = 0; rr < 2; ++rr) {
+          const int row = ks2 * 16 + rr * 8 + tr_row;
+          const int d = db * 32 + tr_col;
+          const int c = d >> 3;
+          const int off = row * ROWB + ((c ^ ((row & 3) << 2)) << 4) + ((d & 7) << 1);
+          t2[rr] = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4_t *)(vb_lds + off));
+        }
+        const u32x4_t aw = {__builtin_bit_cast(u32x2_t, t2[0])[0],
+                            __builtin_bit_cast(u32x2_t, t2[0])[1],
+                            __builtin_bit_cast(u32x2_t, t2[1])[0],
+                            __builtin_bit_cast(u32x2_t, t2[1])[1]};
+        acc_o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, aw),
+                                                            bop, acc_o[db], 0, 0, 0);
+      }
+    }
+  };
+
+  // ---- 3-stage ring, unrolled so that every stage is a distinct LDS object.
+  // At the top of a step this thread waits for its own copies of tile kt
+  // (those of tile kt + 64, issued later, may stay in flight: 2 * NJ
+  // instructions), then the barrier makes every thread's copies visible and
+  // guarantees that the stage of tile kt - 64 is no longer read.
+  auto step = [&](int kt, const uint8_t *kc, const uint8_t *vc, uint8_t *kn, uint8_t *vn) {
+    static_assert(2 * NJ == 4, "vmcnt immediate below assumes 4 copies per tile");
+    if (kt + kKT <= kt_last)
+      __builtin_amdgcn_s_waitcnt(0xF74);  // vmcnt(4) expcnt(7) lgkmcnt(15)
+    else
+      __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+    if (kt + 2 * kKT <= kt_last) issue_tile(kt + 2 * kKT, kn, vn);
+    compute_tile(kt, kc, vc);
+  };
+  if (any_key) {
+    issue_tile(kt0, k_lds0, v_lds0);
+    if (kt0 + kKT <= kt_last) issue_tile(kt0 + kKT, k_lds1, v_lds1);
+    for (int kt = kt0;;) {
+      step(kt, k_lds0, v_lds0, k_lds2, v_lds2);
+      kt += kKT;
+      if (kt > kt_last) break;
+      step(kt, k_lds1, v_lds1, k_lds0, v_lds0);
+      kt += kKT;
+      if (kt > kt_last) break;
+      step(kt, k_lds2, v_lds2, k_lds1, v_lds1);
+      kt += kKT;
+      if (kt > kt_last) break;
+    }
+  }
+
+  l_run += __shfl_xor(l_run, 32, 64);
+  float oscale = 1.0f;
+  float denom = l_run;
+  if (p.sink) {
+    const float sink2 = p.sink[row_ok ? hq : 0] * kLog2e;
+    const float M = fmaxf(m_run, sink2);
+    const float f = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - M);
+    denom = l_run * f + __builtin_amdgcn_exp2f(sink2 - M);
+    oscale = f;
+  }
+  const float vscale = p.v_deq ? p.v_deq[h] : 1.0f;
+  const float inv = (denom > 0.f) ? oscale * vscale / denom : 0.f;
+  if (row_ok) {
+    uint16_t *op = p.out + (int64_t)(q_begin + pos_r) * p.os_t + (int64_t)hq * p.os_h;
+#pragma unroll
+    for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const int d0 = db * 32 + e4 * 8 + half * 4;
+        const u32x2_t w = {pack2_bf16(acc_o[db][e4 * 4] * inv, acc_o[db][e4 * 4 + 1] * inv),
+                           pack2_bf16(acc_o[db][e4 * 4 + 2] * inv, acc_o[db][e4 * 4 + 3] * inv)};
+        *reinterpret_cast<u32x2_t *>(op + d0) = w;
+      }
+  }
+}
+
 }  // namespace
 
 int launch_paged_prefill(const mia_prefill_args &a, hipStream_t s) {
@@ -411,6 +740,12 @@ int launch_paged_prefill(const mia_prefill_args &a, hipStream_t s) {
                   (unsigned)a.num_seqs);
   if (a.head_dim == 128) {
     if (fp8) hipLaunchKernelGGL((prefill_kernel<128, true>), grid, dim3(256), 0, s, kp);
+    else if (a.block_size % 16 == 0 && (64 % a.block_size == 0 || a.block_size % 64 == 0) &&
+             a.blocks_per_seq <= kDmaIds) {
+      const dim3 g2((unsigned)((rows + kDmaRows - 1) / kDmaRows), (unsigned)a.num_kv_heads,
+                    (unsigned)a.num_seqs);
+      hipLaunchKernelGGL((prefill_dma_kernel<128>), g2, dim3(kDmaWaves * 64), 0, s, kp);
+    }
     else hipLaunchKernelGGL((prefill_kernel<128, false>), grid, dim3(256), 0, s, kp);
   } else {
     if (fp8) hipLaunchKernelGGL((prefill_kernel<64, true>), grid, dim3(256), 0, s, kp);
