@@ -299,8 +299,19 @@ typedef struct {
   int32_t num_tokens;     /* rows of q / out; rows at or past it are skipped */
   void *out;
   int64_t out_stride[3]; /* token, hq, d */
+  /* Split-K over keys: a long sequence's keys are cut into chunks of
+   * split_tokens (a multiple of 64; 0 = chosen from the shapes) processed by
+   * separate workgroups, whose fp32 partials go to `workspace` and are
+   * merged by a second kernel.  workspace_bytes must be at least
+   * mia_prefill_workspace_bytes(args) (0 when no split is planned; then
+   * workspace may be NULL). */
+  void *workspace;
+  size_t workspace_bytes;
+  int32_t split_tokens;
+  int32_t _pad0;
 } mia_prefill_args;
 
+size_t mia_prefill_workspace_bytes(const mia_prefill_args *args);
 int mia_paged_prefill(const mia_prefill_args *args, mia_stream_t stream);
 
 /* ------------------------------------------------------------------------ */

@@ -157,3 +157,75 @@ def test_prefill_empty_and_fully_masked(gpu):
     v = _seq_kv(b.v_cache.cpu(), b.block_table[0].cpu(), 40, 2)  # [2, 40, 64]
     ref = v.repeat_interleave(4, 0).transpose(0, 1)
     assert (out.float().cpu() - ref.float()).abs().max().item() <= 1e-2
+
+
+SPLIT_CASES = [
+    # q_heads, kv_heads, d, bs, new, priors, window, sink, fp8
+    (32, 8, 128, 32, 256, [1500, 96, 700], 0, False, False),   # copy-ring kernel
+    (16, 2, 128, 32, 200, [900, 0], 0, True, False),
+    (16, 2, 64, 32, 160, [1200, 64], 64, True, False),         # d = 64 kernel, window
+    (12, 2, 128, 64, 128, [1024, 320], 0, False, True),        # fp8 cache
+]
+
+
+@pytest.mark.parametrize("case", range(len(SPLIT_CASES)))
+@pytest.mark.parametrize("split", [64, 192, 512])
+def test_split_keys_match_unsplit_and_reference(gpu, case, split):
+    """Key ranges cut into chunks of `split` keys (partials merged by the
+    combine kernel) give the unsplit result, and both match the reference
+    per sequence; sequences of very different lengths share the launch."""
+    Hq, Hkv, d, bs, S, priors, win, use_sink, fp8 = SPLIT_CASES[case]
+    pmax = max(priors)  # pool and table sized for the longest sequence
+    cfg = W.PrefillConfig("s", len(priors), Hq, Hkv, d, bs, S, pmax, pmax, fp8=fp8,
+                          seed=90 + case)
+    b = W.make_prefill_batch(cfg, gpu)
+    # replace the priors (the generator draws one value for every sequence)
+    pr = torch.tensor(priors, dtype=torch.int32)
+    tot = pr + S
+    nblk = b.block_table.shape[1]
+    need = int(((tot + bs - 1) // bs).max())
+    if need > nblk:
+        pytest.skip("table too narrow for the chosen priors")
+    kw = {}
+    if fp8:
+        kw = dict(k_dequant=b.k_dequant, v_dequant=b.v_dequant)
+        K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache, quant_mode=2,
+                   k_scale=b.k_quant, v_scale=b.v_quant, scale_per_head=True)
+    # fresh table: every sequence gets distinct random blocks for its span
+    nb = b.k_cache.shape[0]
+    g = torch.Generator().manual_seed(5 + case)
+    perm = torch.randperm(nb - 1, generator=g) + 1
+    table = torch.full((len(priors), nblk), -1, dtype=torch.int32)
+    off = 0
+    for i in range(len(priors)):
+        n = int((tot[i] + bs - 1) // bs)
+        if off + n > nb - 1:
+            pytest.skip("pool too small for the chosen priors")
+        table[i, :n] = perm[off:off + n].to(torch.int32)
+        off += n
+    table = table.to(gpu)
+    prior = pr.to(gpu)
+    sink = torch.randn(Hq, generator=g).to(gpu) if use_sink else None
+    scale = d ** -0.5
+    base = K.paged_prefill(b.q, b.cu_seqlens, prior, S, b.k_cache, b.v_cache, table,
+                           scale=scale, sliding_window=win, sink=sink,
+                           split_tokens=1 << 20, **kw)
+    out = K.paged_prefill(b.q, b.cu_seqlens, prior, S, b.k_cache, b.v_cache, table,
+                          scale=scale, sliding_window=win, sink=sink, split_tokens=split, **kw)
+    # chunks keep their own running max, so the bf16 rounding of the
+    # probabilities differs: allow two bf16 ulps at |o| ~ 2
+    assert (out.float() - base.float()).abs().max().item() <= 1.6e-2
+    tol = TOL_FP8 if fp8 else TOL_BF16
+    for i in range(len(priors)):
+        s0, s1 = int(b.cu_seqlens[i]), int(b.cu_seqlens[i + 1])
+        n = int(tot[i])
+        kc, vc = b.k_cache.cpu(), b.v_cache.cpu()
+        if fp8:
+            kc = kc.float() * b.k_dequant.cpu().view(1, -1, 1, 1)
+            vc = vc.float() * b.v_dequant.cpu().view(1, -1, 1, 1)
+        ks = _seq_kv(kc, table[i].cpu(), n, Hkv)
+        vs = _seq_kv(vc, table[i].cpu(), n, Hkv)
+        f = OSg.fp32_prefill(b.q[s0:s1].cpu(), ks, vs, priors[i], scale, win,
+                             None if sink is None else sink.cpu())
+        err = (out[s0:s1].float().cpu().double() - f).abs().max().item()
+        assert err <= tol, (i, err)

@@ -205,10 +205,7 @@ int mia_paged_decode(const mia_decode_args *a, mia_stream_t stream) {
   return mia::launch_paged_decode(*a, pl, (hipStream_t)stream);
 }
 
-int mia_paged_prefill(const mia_prefill_args *a, mia_stream_t stream) {
-  mia::g_last_error.clear();
-  MIA_REQUIRE(a, MIA_ERR_VALUE, "prefill: null args");
-  if (a->num_seqs == 0) return MIA_OK;
+static int validate_prefill(const mia_prefill_args *a) {
   MIA_REQUIRE(a->q && a->cu_seqlens_q && a->prior_tokens && a->k_cache &&
                   a->v_cache && a->block_table && a->out,
               MIA_ERR_VALUE, "prefill: null tensor pointer");
@@ -245,7 +242,31 @@ int mia_paged_prefill(const mia_prefill_args *a, mia_stream_t stream) {
                   (a->out_stride[1] * 2) % 8 == 0,
               MIA_ERR_VALUE, "prefill: output must be bf16 with contiguous d");
   MIA_REQUIRE(a->max_seqlen_q >= 0, MIA_ERR_VALUE, "prefill: max_seqlen_q < 0");
-  return mia::launch_paged_prefill(*a, (hipStream_t)stream);
+  MIA_REQUIRE(a->split_tokens >= 0, MIA_ERR_VALUE, "prefill: negative split_tokens");
+  return MIA_OK;
+}
+
+size_t mia_prefill_workspace_bytes(const mia_prefill_args *a) {
+  mia::g_last_error.clear();
+  if (!a || a->num_seqs == 0) return 0;
+  if (validate_prefill(a) != MIA_OK) return 0;
+  return mia::plan_prefill(*a).ws_bytes;
+}
+
+int mia_paged_prefill(const mia_prefill_args *a, mia_stream_t stream) {
+  mia::g_last_error.clear();
+  MIA_REQUIRE(a, MIA_ERR_VALUE, "prefill: null args");
+  if (a->num_seqs == 0) return MIA_OK;
+  int rc = validate_prefill(a);
+  if (rc) return rc;
+  const mia::PrefillPlan pl = mia::plan_prefill(*a);
+  if (pl.ws_bytes > 0) {
+    MIA_REQUIRE(a->workspace && a->workspace_bytes >= pl.ws_bytes, MIA_ERR_VALUE,
+                "prefill: workspace too small (query mia_prefill_workspace_bytes)");
+    MIA_REQUIRE(aligned(a->workspace, 16), MIA_ERR_VALUE,
+                "prefill: workspace must be 16-byte aligned");
+  }
+  return mia::launch_paged_prefill(*a, pl, (hipStream_t)stream);
 }
 
 static void slot_mapping_one(const mia_slot_mapping_args *a, int64_t t) {

@@ -43,6 +43,17 @@ DecodePlan plan_decode(const mia_decode_args &a);
 int launch_paged_decode(const mia_decode_args &a, const DecodePlan &p,
                         hipStream_t s);
 
-int launch_paged_prefill(const mia_prefill_args &a, hipStream_t s);
+// Paged prefill: split-K plan shared by the workspace query and the launch.
+struct PrefillPlan {
+  bool dma;          // bf16 / head_dim 128 kernel with the LDS copy ring
+  int rows_wg;       // query rows per workgroup
+  int rows_max;      // max_seqlen_q * G
+  int nsplit;        // key chunks per row tile at most (1: no split)
+  int ksplit;        // keys per chunk (0: chosen on the device)
+  int slots;         // workgroups resident on the device at once
+  size_t ws_bytes;   // workspace bytes (0 without split)
+};
+PrefillPlan plan_prefill(const mia_prefill_args &a);
+int launch_paged_prefill(const mia_prefill_args &a, const PrefillPlan &p, hipStream_t s);
 
 }  // namespace mia

@@ -69,7 +69,117 @@ struct PrefillKParams {
   int num_tokens;
   uint16_t *out;
   int64_t os_t, os_h;
+  // split-K over keys (nsplit == 1: off)
+  float *ws;      // [num_seqs, Hkv, rows_max, nsplit, D + 2] fp32 partials
+  int nsplit;     // chunks per row tile at most (grid z = nsplit * num_seqs)
+  int num_seqs;
+  int ksplit;     // keys per chunk (multiple of the 64-key tile)
+  int slots;      // workgroups resident on the device at once
+  int rows_wg;    // query rows per workgroup of the attention kernel
+  int rows_max;   // max_seqlen_q * G
 };
+
+MIA_DEV uint32_t pack2_bf16(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)a, (__bf16)b};  // round to nearest even
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Key range of the workgroup whose rows start at row0 (rows are GQA-packed:
+// row = pos * G + g): tiles kt0 .. kt_last (64-key aligned) and the number
+// of key chunks it spans.  Shared by the attention and combine kernels so
+// that both agree on which rows were split.
+struct KeyRange {
+  int kmin, kmax;       // keys visible to some row
+  int kt0, kt_last;     // first / last tile
+  int n_sp;             // chunks of ksplit keys covering the tiles
+  bool any;
+};
+
+MIA_DEV KeyRange wg_key_range(const PrefillKParams &p, int prior, int S_q, int row0,
+                              int ksplit) {
+  KeyRange k;
+  const int s_ctx = p.nblk * p.bs;
+  const int pos_lo = row0 / p.G;
+  const int pos_hi = min(S_q - 1, (row0 + p.rows_wg - 1) / p.G);
+  k.kmax = min(min(prior + pos_hi + 1, prior + S_q), s_ctx);
+  k.kmin = p.window > 0 ? max(0, prior + pos_lo - p.window + 1) : 0;
+  k.any = k.kmax > k.kmin;
+  k.kt0 = (k.kmin / kKT) * kKT;
+  k.kt_last = k.kmax > k.kt0 ? ((k.kmax - 1) / kKT) * kKT : k.kt0;
+  k.n_sp = (k.any && p.nsplit > 1) ? k.kt_last / ksplit - k.kt0 / ksplit + 1 : 1;
+  return k;
+}
+
+MIA_DEV int split_keys(const PrefillKParams &p) {
+  return p.nsplit <= 1 ? (1 << 30) : p.ksplit;
+}
+
+// Epilogue shared by the attention kernels.  Lane holds O^T[d][row] for
+// d = db*32 + (e/4)*8 + half*4 + e%4 of its row (lane % 32); m_run / l_run
+// are the row's running max (log2 domain) and this lane's partial sum.
+// Unsplit rows are normalised (sink in the denominator only, rows with no
+// visible key -> 0) and stored as bf16; split rows store the fp32 partial
+// (o * vscale, m, l) of chunk sp for prefill_combine_kernel.
+// Normalises one row (sink in the denominator only; a row with no visible
+// key gives 0) and stores it as bf16.  l_run is the row's full sum.
+template <int D>
+MIA_DEV void store_final(const PrefillKParams &p, const f32x16_t (&acc_o)[D / 32], float m_run,
+                         float l_run, bool row_ok, int hq, int64_t tok, int half,
+                         float vscale) {
+  float oscale = 1.0f;
+  float denom = l_run;
+  if (p.sink) {
+    const float sink2 = p.sink[row_ok ? hq : 0] * kLog2e;
+    const float M = fmaxf(m_run, sink2);
+    const float f = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - M);
+    denom = l_run * f + __builtin_amdgcn_exp2f(sink2 - M);
+    oscale = f;
+  }
+  const float inv = (denom > 0.f) ? oscale * vscale / denom : 0.f;
+  if (row_ok) {
+    uint16_t *op = p.out + tok * p.os_t + (int64_t)hq * p.os_h;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int e4 = 0; e4 < 4; ++e4) {
+        const int d0 = db * 32 + e4 * 8 + half * 4;
+        const u32x2_t w = {pack2_bf16(acc_o[db][e4 * 4] * inv, acc_o[db][e4 * 4 + 1] * inv),
+                           pack2_bf16(acc_o[db][e4 * 4 + 2] * inv, acc_o[db][e4 * 4 + 3] * inv)};
+        *reinterpret_cast<u32x2_t *>(op + d0) = w;
+      }
+  }
+}
+
+template <int D>
+MIA_DEV void finish_rows(const PrefillKParams &p, const f32x16_t (&acc_o)[D / 32], float m_run,
+                         float l_run, bool row_ok, int seq, int h, int hq, int64_t tok,
+                         int r, int half, int n_sp, int sp, float vscale) {
+  l_run += __shfl_xor(l_run, 32, 64);
+  if (n_sp > 1) {
+    // split row tile: store this chunk's partial (o * vscale, m, l) for
+    // prefill_combine_kernel
+    if (row_ok) {
+      float *w = p.ws + ((((int64_t)seq * p.Hkv + h) * p.rows_max + r) * p.nsplit + sp) *
+                            (int64_t)(D + 2);
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+        for (int e4 = 0; e4 < 4; ++e4) {
+          const int d0 = db * 32 + e4 * 8 + half * 4;
+          *reinterpret_cast<f32x4_t *>(w + d0) =
+              f32x4_t{acc_o[db][e4 * 4] * vscale, acc_o[db][e4 * 4 + 1] * vscale,
+                      acc_o[db][e4 * 4 + 2] * vscale, acc_o[db][e4 * 4 + 3] * vscale};
+        }
+      if (half == 0) {
+        w[D] = m_run;
+        w[D + 1] = l_run;
+      }
+    }
+    return;
+  }
+  store_final<D>(p, acc_o, m_run, l_run, row_ok, hq, tok, half, vscale);
+}
 
 // 8 cache elements as 8 bf16 (4 packed dwords) — raw register form and
 // its conversion.  fp8 values come out scaled by 2^-8 (exact).
@@ -99,11 +209,6 @@ struct Chunk8<true> {
   }
 };
 
-MIA_DEV uint32_t pack2_bf16(float a, float b) {
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  const bf16x2_t v = {(__bf16)a, (__bf16)b};  // round to nearest even
-  return __builtin_bit_cast(uint32_t, v);
-}
 
 template <int D, bool FP8>
 __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
@@ -121,7 +226,10 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[kKT * KROW];
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[D * VROW];
 
-  const int seq = blockIdx.z;
+  // chunk-major grid: the workgroups of high chunk indices, which exit at
+  // once for row tiles with fewer chunks, are dispatched last
+  const int sp = blockIdx.z / p.num_seqs;  // key chunk of a split row tile
+  const int seq = blockIdx.z - sp * p.num_seqs;
   const int h = blockIdx.y;
   const int G = p.G;
   const int q_begin = p.cu[seq];
@@ -129,6 +237,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
   const int rows_total = S_q * G;
   const int row0 = blockIdx.x * kRowsWG;
   if (row0 >= rows_total) return;
+  const int ksplit = split_keys(p);
   const int prior = p.prior[seq];
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -184,8 +293,14 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
   // (chunk c of 4 keys goes to slot [0, 2, 1, 3][c]) to match the P^T layout
   const int v_col = (vg >> 2) * 16 + (((vg & 1) << 1) | ((vg >> 1) & 1)) * 4;
 
-  const int kt0 = (kmin / kKT) * kKT;
-  const int kt_last = kmax > kt0 ? ((kmax - 1) / kKT) * kKT : kt0;
+  const KeyRange kr = wg_key_range(p, prior, S_q, row0, ksplit);
+  if (sp >= kr.n_sp) return;  // no chunk for this workgroup
+  int kt0 = kr.kt0, kt_last = kr.kt_last;
+  if (kr.n_sp > 1) {
+    const int c = kt0 / ksplit + sp;
+    kt0 = max(kt0, c * ksplit);
+    kt_last = min(kt_last, c * ksplit + ksplit - kKT);
+  }
   // clamp a key into [kt0, kmax) so every load hits an attended block
   auto clampk = [&](int k) { return min(max(k, kt0), max(kmax - 1, kt0)); };
   auto phys_of = [&](int key) {
@@ -340,30 +455,8 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
   }
 
   // ---- finalize: lane holds O^T[d = db*32 + (e/4)*8 + half*4 + e%4][row rl]
-  l_run += __shfl_xor(l_run, 32, 64);
-  float oscale = 1.0f;
-  float denom = l_run;
-  if (p.sink) {
-    const float sink2 = p.sink[row_ok ? hq : 0] * kLog2e;
-    const float M = fmaxf(m_run, sink2);
-    const float f = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - M);
-    denom = l_run * f + __builtin_amdgcn_exp2f(sink2 - M);
-    oscale = f;
-  }
-  const float vscale = (p.v_deq ? p.v_deq[h] : 1.0f) * (p.fp8 ? 256.0f : 1.0f);
-  const float inv = (denom > 0.f) ? oscale * vscale / denom : 0.f;
-  if (row_ok) {
-    uint16_t *op = p.out + (int64_t)(q_begin + pos_r) * p.os_t + (int64_t)hq * p.os_h;
-#pragma unroll
-    for (int db = 0; db < DBLK; ++db)
-#pragma unroll
-      for (int e4 = 0; e4 < 4; ++e4) {
-        const int d0 = db * 32 + e4 * 8 + half * 4;
-        const u32x2_t w = {pack2_bf16(acc_o[db][e4 * 4] * inv, acc_o[db][e4 * 4 + 1] * inv),
-                           pack2_bf16(acc_o[db][e4 * 4 + 2] * inv, acc_o[db][e4 * 4 + 3] * inv)};
-        *reinterpret_cast<u32x2_t *>(op + d0) = w;
-      }
-  }
+  finish_rows<D>(p, acc_o, m_run, l_run, row_ok, seq, h, hq, (int64_t)q_begin + pos_r, r, half,
+                 kr.n_sp, sp, (p.v_deq ? p.v_deq[h] : 1.0f) * (p.fp8 ? 256.0f : 1.0f));
 }
 
 // ---------------------------------------------------------------------------
@@ -404,18 +497,17 @@ __global__ __launch_bounds__(512, 1) void prefill_dma_kernel(PrefillKParams p) {
   typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
   typedef __attribute__((address_space(3))) void lds_void_t;
 
-  // One __shared__ object per stage: the compiler then sees that a copy
-  // into one stage cannot alias the reads of another and does not wait for
-  // it before computing.
   __shared__ int32_t ids_lds[kDmaIds];
-  __shared__ __attribute__((aligned(1024))) uint8_t k_lds0[TILEB];
-  __shared__ __attribute__((aligned(1024))) uint8_t k_lds1[TILEB];
-  __shared__ __attribute__((aligned(1024))) uint8_t k_lds2[TILEB];
-  __shared__ __attribute__((aligned(1024))) uint8_t v_lds0[TILEB];
-  __shared__ __attribute__((aligned(1024))) uint8_t v_lds1[TILEB];
-  __shared__ __attribute__((aligned(1024))) uint8_t v_lds2[TILEB];
+  __shared__ __attribute__((aligned(1024))) uint8_t kv_lds[3][2][TILEB];  // [stage][K, V]
+  // LDS addresses are handled as LDS pointers / integers only: a generic
+  // pointer to shared memory carried through the loops would need the
+  // aperture conversion at every use
+  lds_u8_t *const kv_base = (lds_u8_t *)&kv_lds[0][0][0];
 
-  const int seq = blockIdx.z;
+  // chunk-major grid: the workgroups of high chunk indices, which exit at
+  // once for row tiles with fewer chunks, are dispatched last
+  const int sp = blockIdx.z / p.num_seqs;  // key chunk of a split row tile
+  const int seq = blockIdx.z - sp * p.num_seqs;
   const int h = blockIdx.y;
   const int G = p.G;
   const int q_begin = p.cu[seq];
@@ -423,6 +515,7 @@ __global__ __launch_bounds__(512, 1) void prefill_dma_kernel(PrefillKParams p) {
   const int rows_total = S_q * G;
   const int row0 = blockIdx.x * kDmaRows;
   if (row0 >= rows_total) return;
+  const int ksplit = split_keys(p);
   const int prior = p.prior[seq];
   const int tid = threadIdx.x;
   const int wave = readfirstlane(tid >> 6);
@@ -446,8 +539,14 @@ __global__ __launch_bounds__(512, 1) void prefill_dma_kernel(PrefillKParams p) {
   const int full_hi = min(min(prior + pos_lo + 1, prior + S_q), s_ctx);
   const int full_lo = p.window > 0 ? prior + pos_hi - p.window + 1 : 0;
   const bool any_key = kmax > kmin;
-  const int kt0 = (kmin / kKT) * kKT;
-  const int kt_last = kmax > kt0 ? ((kmax - 1) / kKT) * kKT : kt0;
+  const KeyRange kr = wg_key_range(p, prior, S_q, row0, ksplit);
+  if (sp >= kr.n_sp) return;  // no chunk for this workgroup
+  int kt0 = kr.kt0, kt_last = kr.kt_last;
+  if (kr.n_sp > 1) {
+    const int c = kt0 / ksplit + sp;
+    kt0 = max(kt0, c * ksplit);
+    kt_last = min(kt_last, c * ksplit + ksplit - kKT);
+  }
 
   bf16x8_t qf[KSTEPS];
   {
@@ -488,13 +587,13 @@ __global__ __launch_bounds__(512, 1) void prefill_dma_kernel(PrefillKParams p) {
   const int dma_s = lane & 15;
   const uint8_t *k_head = p.k_cache + (int64_t)h * p.kc_h * 2;
   const uint8_t *v_head = p.v_cache + (int64_t)h * p.vc_h * 2;
-  int64_t k_lane[NJ], v_lane[NJ];
+  int32_t k_lane[NJ], v_lane[NJ];  // bytes inside a block: < block_size * 256
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int row = 4 * (kDmaWaves * j + wave) + dma_r;
     const int roff = row % p.bs;
-    k_lane[j] = (int64_t)roff * p.kc_t * 2 + ((dma_s ^ (row & 15)) << 4);
-    v_lane[j] = (int64_t)roff * p.vc_t * 2 + ((dma_s ^ ((row & 3) << 2)) << 4);
+    k_lane[j] = roff * (int)p.kc_t * 2 + ((dma_s ^ (row & 15)) << 4);
+    v_lane[j] = roff * (int)p.vc_t * 2 + ((dma_s ^ ((row & 3) << 2)) << 4);
   }
   // One 16-byte-per-lane copy HBM -> LDS (global_load_lds_dwordx4): lane
   // data lands at lds_dst + 16 * lane.  Issued through inline assembly so
@@ -502,9 +601,8 @@ __global__ __launch_bounds__(512, 1) void prefill_dma_kernel(PrefillKParams p) {
   // not add waits before reads of other stages; the waits for these copies
   // are the explicit s_waitcnt in `step` below.
   // M0 (the LDS base of the copy) is saved and restored around it.
-  auto dma16 = [&](const uint8_t *src, uint8_t *lds_dst) {
-    const uint32_t m0 =
-        readfirstlane((int)(uint32_t)(uintptr_t)(lds_void_t *)lds_dst);
+  auto dma16 = [&](const uint8_t *src, uint32_t lds_dst) {
+    const uint32_t m0 = readfirstlane((int)lds_dst);
     uint32_t saved;
     asm volatile(
         "s_mov_b32 %0, m0\n\t"
@@ -515,7 +613,7 @@ __global__ __launch_bounds__(512, 1) void prefill_dma_kernel(PrefillKParams p) {
         : "s"(m0), "v"(src)
         : "memory");
   };
-  auto issue_tile = [&](int kt, uint8_t *k_dst, uint8_t *v_dst) {
+  auto issue_tile = [&](int kt, uint32_t k_dst, uint32_t v_dst) {
     const int ktoff = kt - (int)fdiv((uint32_t)kt, p.bs_div) * p.bs;  // kt % bs
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
@@ -542,9 +640,7 @@ __global__ __launch_bounds__(512, 1) void prefill_dma_kernel(PrefillKParams p) {
   const int tr_col = ((lane >> 4) & 1) * 16 + 4 * (tr_k & 3);
   const int tr_row = half * 4 + (tr_k >> 2);
 
-  auto compute_tile = [&](int kt, const uint8_t *k_src, const uint8_t *v_src) {
-    const lds_u8_t *kb_lds = (const lds_u8_t *)k_src;
-    const lds_u8_t *vb_lds = (const lds_u8_t *)v_src;
+  auto compute_tile = [&](int kt, const lds_u8_t *kb_lds, const lds_u8_t *vb_lds) {
     // ---- S^T = K . Q^T
     f32x16_t sacc[2];
 #pragma unroll
@@ -636,68 +732,181 @@ __global__ __launch_bounds__(512, 1) void prefill_dma_kernel(PrefillKParams p) {
     }
   };
 
-  // ---- 3-stage ring, unrolled so that every stage is a distinct LDS object.
-  // At the top of a step this thread waits for its own copies of tile kt
-  // (those of tile kt + 64, issued later, may stay in flight: 2 * NJ
-  // instructions), then the barrier makes every thread's copies visible and
-  // guarantees that the stage of tile kt - 64 is no longer read.
-  auto step = [&](int kt, const uint8_t *kc, const uint8_t *vc, uint8_t *kn, uint8_t *vn) {
-    static_assert(2 * NJ == 4, "vmcnt immediate below assumes 4 copies per tile");
-    if (kt + kKT <= kt_last)
-      __builtin_amdgcn_s_waitcnt(0xF74);  // vmcnt(4) expcnt(7) lgkmcnt(15)
-    else
-      __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-    if (kt + 2 * kKT <= kt_last) issue_tile(kt + 2 * kKT, kn, vn);
-    compute_tile(kt, kc, vc);
-  };
+  // ---- 3-stage ring.  At the top of a step this thread waits for its own
+  // copies of tile kt (those of tile kt + 64, issued later, may stay in
+  // flight: 2 * NJ instructions), then the barrier makes every thread's
+  // copies visible and guarantees that the stage of tile kt - 64, which the
+  // step refills, is no longer read.
   if (any_key) {
-    issue_tile(kt0, k_lds0, v_lds0);
-    if (kt0 + kKT <= kt_last) issue_tile(kt0 + kKT, k_lds1, v_lds1);
-    for (int kt = kt0;;) {
-      step(kt, k_lds0, v_lds0, k_lds2, v_lds2);
-      kt += kKT;
-      if (kt > kt_last) break;
-      step(kt, k_lds1, v_lds1, k_lds0, v_lds0);
-      kt += kKT;
-      if (kt > kt_last) break;
-      step(kt, k_lds2, v_lds2, k_lds1, v_lds1);
-      kt += kKT;
-      if (kt > kt_last) break;
+    const uint32_t lds0 = (uint32_t)(uintptr_t)kv_base;
+    auto k_at = [&](int stg) { return lds0 + (uint32_t)(stg * 2 * TILEB); };
+    issue_tile(kt0, k_at(0), k_at(0) + TILEB);
+    if (kt0 + kKT <= kt_last) issue_tile(kt0 + kKT, k_at(1), k_at(1) + TILEB);
+    int st = 0;
+    for (int kt = kt0; kt <= kt_last; kt += kKT) {
+      static_assert(2 * NJ == 4, "vmcnt immediate below assumes 4 copies per tile");
+      if (kt + kKT <= kt_last)
+        __builtin_amdgcn_s_waitcnt(0xF74);  // vmcnt(4) expcnt(7) lgkmcnt(15)
+      else
+        __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      const int st2 = st >= 1 ? st - 1 : 2;  // (st + 2) % 3
+      if (kt + 2 * kKT <= kt_last) issue_tile(kt + 2 * kKT, k_at(st2), k_at(st2) + TILEB);
+      compute_tile(kt, kv_base + st * 2 * TILEB, kv_base + st * 2 * TILEB + TILEB);
+      st = st == 2 ? 0 : st + 1;
     }
   }
 
-  l_run += __shfl_xor(l_run, 32, 64);
-  float oscale = 1.0f;
-  float denom = l_run;
-  if (p.sink) {
-    const float sink2 = p.sink[row_ok ? hq : 0] * kLog2e;
-    const float M = fmaxf(m_run, sink2);
-    const float f = (m_run == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_run - M);
-    denom = l_run * f + __builtin_amdgcn_exp2f(sink2 - M);
-    oscale = f;
+  finish_rows<D>(p, acc_o, m_run, l_run, row_ok, seq, h, hq, (int64_t)q_begin + pos_r, r, half,
+                 kr.n_sp, sp, p.v_deq ? p.v_deq[h] : 1.0f);
+}
+
+// ---------------------------------------------------------------------------
+// split-K merge
+// ---------------------------------------------------------------------------
+// One wave per query row (4 rows per workgroup); rows of tiles that were
+// not split exit at once.  The n_sp partials (o, m, l) of the row (log2
+// domain) are loaded together, the sink joins the denominator, and the
+// bf16 row is written.
+// Merge of the split rows: 16 rows per workgroup (grid over all rows;
+// rows of unsplit tiles exit at once); each wave loads the n_sp partials
+// (o, m, l) of its 4 rows together (log2 domain), adds the sink to the
+// denominator and writes the bf16 rows.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillKParams p) {
+  constexpr int DPL = D / 64;  // d values per lane
+  constexpr int kMaxSp = 8;
+  constexpr int RPW = 4;       // rows per wave, loaded together
+  const int seq = blockIdx.z;
+  const int h = blockIdx.y;
+  const int q_begin = p.cu[seq];
+  const int S_q = p.cu[seq + 1] - q_begin;
+  const int rows_total = S_q * p.G;
+  const int r0 = blockIdx.x * 16;  // inside one row tile (rows_wg % 16 == 0)
+  if (r0 >= rows_total) return;
+  const KeyRange kr =
+      wg_key_range(p, p.prior[seq], S_q, (r0 / p.rows_wg) * p.rows_wg, split_keys(p));
+  if (kr.n_sp <= 1) return;
+  const int n_sp = min(kr.n_sp, kMaxSp);
+  const int lane = threadIdx.x & 63;
+  const int rw = r0 + (threadIdx.x >> 6) * RPW;
+  if (rw >= rows_total) return;
+  float m[RPW][kMaxSp], l[RPW][kMaxSp], o[RPW][kMaxSp][DPL];
+#pragma unroll
+  for (int i = 0; i < RPW; ++i) {
+    const int r = min(rw + i, rows_total - 1);
+    const float *w0 =
+        p.ws + (((int64_t)seq * p.Hkv + h) * p.rows_max + r) * p.nsplit * (int64_t)(D + 2);
+#pragma unroll
+    for (int j = 0; j < kMaxSp; ++j) {
+      const float *w = w0 + min(j, n_sp - 1) * (D + 2);
+      m[i][j] = w[D];
+      l[i][j] = w[D + 1];
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) o[i][j][e] = w[lane * DPL + e];
+    }
   }
-  const float vscale = p.v_deq ? p.v_deq[h] : 1.0f;
-  const float inv = (denom > 0.f) ? oscale * vscale / denom : 0.f;
-  if (row_ok) {
-    uint16_t *op = p.out + (int64_t)(q_begin + pos_r) * p.os_t + (int64_t)hq * p.os_h;
 #pragma unroll
-    for (int db = 0; db < DBLK; ++db)
+  for (int i = 0; i < RPW; ++i) {
+    const int r = rw + i;
+    if (r >= rows_total) break;
+    const int pos_r = r / p.G;
+    const int hq = h * p.G + (r - pos_r * p.G);
+    if (q_begin + pos_r >= p.num_tokens) continue;
+    const float sink2 = p.sink ? p.sink[hq] * kLog2e : -INFINITY;
+    float M = sink2;
 #pragma unroll
-      for (int e4 = 0; e4 < 4; ++e4) {
-        const int d0 = db * 32 + e4 * 8 + half * 4;
-        const u32x2_t w = {pack2_bf16(acc_o[db][e4 * 4] * inv, acc_o[db][e4 * 4 + 1] * inv),
-                           pack2_bf16(acc_o[db][e4 * 4 + 2] * inv, acc_o[db][e4 * 4 + 3] * inv)};
-        *reinterpret_cast<u32x2_t *>(op + d0) = w;
+    for (int j = 0; j < kMaxSp; ++j)
+      if (j < n_sp) M = fmaxf(M, m[i][j]);
+    const float Mu = (M == -INFINITY) ? 0.f : M;
+    float L = __builtin_amdgcn_exp2f(sink2 - Mu);
+    float acc[DPL];
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxSp; ++j) {
+      if (j < n_sp) {
+        const float f = __builtin_amdgcn_exp2f(m[i][j] - Mu);
+        L += l[i][j] * f;
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) acc[e] += o[i][j][e] * f;
       }
+    }
+    const float inv = L > 0.f ? 1.0f / L : 0.f;
+    uint16_t *op = p.out + (int64_t)(q_begin + pos_r) * p.os_t + (int64_t)hq * p.os_h;
+    if constexpr (DPL == 2) {
+      *reinterpret_cast<uint32_t *>(op + lane * 2) = pack2_bf16(acc[0] * inv, acc[1] * inv);
+    } else {
+      op[lane] = (uint16_t)f32_to_bf16_bits(acc[0] * inv);
+    }
   }
 }
 
 }  // namespace
 
-int launch_paged_prefill(const mia_prefill_args &a, hipStream_t s) {
+namespace {
+
+int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
+}
+
+bool use_dma_kernel(const mia_prefill_args &a) {
+  return a.head_dim == 128 && a.cache_dtype == MIA_DTYPE_BF16 && a.block_size % 16 == 0 &&
+         (64 % a.block_size == 0 || a.block_size % 64 == 0) && a.blocks_per_seq <= kDmaIds;
+}
+
+}  // namespace
+
+PrefillPlan plan_prefill(const mia_prefill_args &a) {
+  PrefillPlan pl;
+  pl.dma = use_dma_kernel(a);
+  pl.rows_wg = pl.dma ? kDmaRows : kRowsWG;
+  const int G = a.num_q_heads / a.num_kv_heads;
+  pl.rows_max = a.max_seqlen_q * G;
+  const int64_t s_ctx = (int64_t)a.blocks_per_seq * a.block_size;
+  const int64_t base_wgs =
+      (int64_t)((pl.rows_max + pl.rows_wg - 1) / pl.rows_wg) * a.num_kv_heads * a.num_seqs;
+  const int slots = device_cus() * (pl.dma ? 1 : 2);
+  pl.slots = slots;
+  int64_t ks = a.split_tokens;
+  if (ks <= 0) {
+    // Without the sequence lengths on the host, split only long tables
+    // (>= 3072 keys) when the row tiles alone do not fill the device twice:
+    // chunks of a third of the table (rounded up to 512 keys), at least
+    // 1024 keys.
+    // A batch whose longest sequence is much longer than the others then
+    // spreads the long one over more workgroups.
+    ks = (s_ctx >= 3072 && base_wgs < 2 * (int64_t)slots)
+             ? std::max<int64_t>(1024, ((s_ctx + 2) / 3 + 511) / 512 * 512)
+             : (int64_t)1 << 30;
+  }
+  ks = std::max<int64_t>(ks, (s_ctx + 7) / 8);  // the merge holds 8 partials
+  ks = std::max<int64_t>(kKT, ((ks + kKT - 1) / kKT) * kKT);
+  pl.ksplit = (int)std::min<int64_t>(ks, 1 << 30);
+  pl.nsplit = s_ctx > 0 ? (int)((s_ctx + pl.ksplit - 1) / pl.ksplit) : 1;
+  if (pl.nsplit <= 1 || (int64_t)a.num_seqs * pl.nsplit > 65535) {
+    pl.nsplit = 1;
+    pl.ws_bytes = 0;
+  } else {
+    pl.ws_bytes = (size_t)a.num_seqs * a.num_kv_heads * pl.rows_max * pl.nsplit *
+                                   (a.head_dim + 2) * sizeof(float);
+  }
+  return pl;
+}
+
+int launch_paged_prefill(const mia_prefill_args &a, const PrefillPlan &pl, hipStream_t s) {
   if (a.num_seqs == 0 || a.max_seqlen_q == 0) return MIA_OK;
   const bool fp8 = a.cache_dtype == MIA_DTYPE_FP8_E4M3FN;
   PrefillKParams kp;
@@ -735,23 +944,33 @@ int launch_paged_prefill(const mia_prefill_args &a, hipStream_t s) {
   kp.out = (uint16_t *)a.out;
   kp.os_t = a.out_stride[0];
   kp.os_h = a.out_stride[1];
-  const int64_t rows = (int64_t)a.max_seqlen_q * kp.G;
-  const dim3 grid((unsigned)((rows + kRowsWG - 1) / kRowsWG), (unsigned)a.num_kv_heads,
-                  (unsigned)a.num_seqs);
-  if (a.head_dim == 128) {
+  kp.ws = (float *)a.workspace;
+  kp.nsplit = pl.nsplit;
+  kp.ksplit = pl.ksplit;
+  kp.slots = pl.slots;
+  kp.num_seqs = a.num_seqs;
+  kp.rows_wg = pl.rows_wg;
+  kp.rows_max = pl.rows_max;
+  const dim3 grid((unsigned)((pl.rows_max + pl.rows_wg - 1) / pl.rows_wg),
+                  (unsigned)a.num_kv_heads, (unsigned)(pl.nsplit * a.num_seqs));
+  if (pl.dma) {
+    hipLaunchKernelGGL((prefill_dma_kernel<128>), grid, dim3(kDmaWaves * 64), 0, s, kp);
+  } else if (a.head_dim == 128) {
     if (fp8) hipLaunchKernelGGL((prefill_kernel<128, true>), grid, dim3(256), 0, s, kp);
-    else if (a.block_size % 16 == 0 && (64 % a.block_size == 0 || a.block_size % 64 == 0) &&
-             a.blocks_per_seq <= kDmaIds) {
-      const dim3 g2((unsigned)((rows + kDmaRows - 1) / kDmaRows), (unsigned)a.num_kv_heads,
-                    (unsigned)a.num_seqs);
-      hipLaunchKernelGGL((prefill_dma_kernel<128>), g2, dim3(kDmaWaves * 64), 0, s, kp);
-    }
     else hipLaunchKernelGGL((prefill_kernel<128, false>), grid, dim3(256), 0, s, kp);
   } else {
     if (fp8) hipLaunchKernelGGL((prefill_kernel<64, true>), grid, dim3(256), 0, s, kp);
     else hipLaunchKernelGGL((prefill_kernel<64, false>), grid, dim3(256), 0, s, kp);
   }
-  return check_hip(hipGetLastError(), "prefill launch");
+  int rc = check_hip(hipGetLastError(), "prefill launch");
+  if (rc || pl.nsplit <= 1) return rc;
+  const dim3 cgrid((unsigned)((pl.rows_max + 15) / 16), (unsigned)a.num_kv_heads,
+                   (unsigned)a.num_seqs);
+  if (a.head_dim == 128)
+    hipLaunchKernelGGL((prefill_combine_kernel<128>), cgrid, dim3(256), 0, s, kp);
+  else
+    hipLaunchKernelGGL((prefill_combine_kernel<64>), cgrid, dim3(256), 0, s, kp);
+  return check_hip(hipGetLastError(), "prefill combine launch");
 }
 
 }  // namespace mia

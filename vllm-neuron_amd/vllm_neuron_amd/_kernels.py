@@ -390,9 +390,15 @@ def paged_prefill(
     k_dequant: Optional[torch.Tensor] = None,
     v_dequant: Optional[torch.Tensor] = None,
     out: Optional[torch.Tensor] = None,
+    split_tokens: int = 0,
+    workspace: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """``q [T, Hq, d]`` (any token/head strides) over paged K/V; sequence i
-    owns rows ``cu_seqlens_q[i]:cu_seqlens_q[i+1]`` and table row i."""
+    owns rows ``cu_seqlens_q[i]:cu_seqlens_q[i+1]`` and table row i.
+
+    Long key ranges are split into chunks of ``split_tokens`` keys (0: chosen
+    from the shapes) whose partials are merged by a second kernel; the
+    partials live in ``workspace`` (allocated here when not given)."""
     dev = N.require_gpu(q, cu_seqlens_q, prior_tokens, k_cache, v_cache, block_table)
     if q.dtype != torch.bfloat16:
         raise NotImplementedError("prefill: q must be bf16")
@@ -459,7 +465,15 @@ def paged_prefill(
     a.num_tokens = T
     a.out = out.data_ptr()
     a.out_stride = _arr(ctypes.c_int64, list(out.stride()))
-    N.check(N.lib().mia_paged_prefill(ctypes.byref(a), N.stream_ptr(dev)), "paged_prefill")
+    a.split_tokens = int(split_tokens)
+    L = N.lib()
+    need = L.mia_prefill_workspace_bytes(ctypes.byref(a))
+    if need:
+        if workspace is None or workspace.numel() * workspace.element_size() < need:
+            workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+        a.workspace = workspace.data_ptr()
+        a.workspace_bytes = need
+    N.check(L.mia_paged_prefill(ctypes.byref(a), N.stream_ptr(dev)), "paged_prefill")
     return out
 
 

@@ -115,6 +115,8 @@ class PrefillArgs(ctypes.Structure):
         ("scale", c_f32), ("sliding_window", c_i32),
         ("sink", c_vp), ("k_dequant", c_vp), ("v_dequant", c_vp),
         ("out_dtype", c_i32), ("num_tokens", c_i32), ("out", c_vp), ("out_stride", c_i64 * 3),
+        ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t),
+        ("split_tokens", c_i32), ("_pad0", c_i32),
     ]
 
 
@@ -161,7 +163,7 @@ ARGS_STRUCTS = {
 EXPORTS = [
     "mia_abi_version", "mia_last_error", "mia_args_size", "mia_kv_write",
     "mia_gather_kv", "mia_decode_mask", "mia_decode_workspace_bytes",
-    "mia_paged_decode", "mia_paged_prefill", "mia_slot_mapping",
+    "mia_paged_decode", "mia_prefill_workspace_bytes", "mia_paged_prefill", "mia_slot_mapping",
     "mia_slot_mapping_host", "mia_remap_null_block", "mia_swa_trim",
     "mia_packed_k_convert", "mia_scatter_rows",
 ]
@@ -186,6 +188,8 @@ def _declare(lib: ctypes.CDLL) -> None:
         fn.restype = c_i32
     lib.mia_decode_workspace_bytes.argtypes = [P(DecodeArgs)]
     lib.mia_decode_workspace_bytes.restype = ctypes.c_size_t
+    lib.mia_prefill_workspace_bytes.argtypes = [P(PrefillArgs)]
+    lib.mia_prefill_workspace_bytes.restype = ctypes.c_size_t
     lib.mia_slot_mapping_host.argtypes = [P(SlotMappingArgs)]
     lib.mia_slot_mapping_host.restype = c_i32
     lib.mia_remap_null_block.argtypes = [c_vp, c_vp, c_i64, c_i32, c_vp]
