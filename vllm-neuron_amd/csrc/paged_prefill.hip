@@ -111,6 +111,31 @@ MIA_DEV KeyRange wg_key_range(const PrefillKParams &p, int prior, int S_q, int r
   return k;
 }
 
+// Workgroups are dispatched to the 8 XCDs round-robin by linear id, and each
+// XCD has its own L2.  The row tiles of one (kv head, chunk-major sequence)
+// group read the same K/V tiles at about the same time, so the linear id is
+// remapped to put all row tiles of a group on one XCD, consecutive groups on
+// consecutive XCDs (group g on XCD g % 8), groups of higher chunk index last
+// within each XCD.  When the group count is not a multiple of 8 the launch
+// order is kept.
+MIA_DEV uint3 xcd_tile() {
+  constexpr uint32_t X = 8;
+  const uint32_t R = gridDim.x;                 // row tiles per group
+  const uint32_t groups = gridDim.y * gridDim.z;
+  const uint32_t L = blockIdx.x + R * (blockIdx.y + gridDim.y * blockIdx.z);
+  uint32_t rt = blockIdx.x, g = blockIdx.y + gridDim.y * blockIdx.z;
+  if (groups % X == 0) {
+    const uint32_t x = L % X, k = L / X;         // k-th workgroup of XCD x
+    rt = k % R;
+    g = (k / R) * X + x;
+  }
+  uint3 t;
+  t.x = rt;
+  t.y = g % gridDim.y;
+  t.z = g / gridDim.y;
+  return t;
+}
+
 MIA_DEV int split_keys(const PrefillKParams &p) {
   return p.nsplit <= 1 ? (1 << 30) : p.ksplit;
 }
@@ -228,14 +253,15 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
 
   // chunk-major grid: the workgroups of high chunk indices, which exit at
   // once for row tiles with fewer chunks, are dispatched last
-  const int sp = blockIdx.z / p.num_seqs;  // key chunk of a split row tile
-  const int seq = blockIdx.z - sp * p.num_seqs;
-  const int h = blockIdx.y;
+  const uint3 tile = xcd_tile();
+  const int sp = tile.z / p.num_seqs;  // key chunk of a split row tile
+  const int seq = tile.z - sp * p.num_seqs;
+  const int h = tile.y;
   const int G = p.G;
   const int q_begin = p.cu[seq];
   const int S_q = p.cu[seq + 1] - q_begin;
   const int rows_total = S_q * G;
-  const int row0 = blockIdx.x * kRowsWG;
+  const int row0 = tile.x * kRowsWG;
   if (row0 >= rows_total) return;
   const int ksplit = split_keys(p);
   const int prior = p.prior[seq];
@@ -506,14 +532,15 @@ __global__ __launch_bounds__(512, 1) void prefill_dma_kernel(PrefillKParams p) {
 
   // chunk-major grid: the workgroups of high chunk indices, which exit at
   // once for row tiles with fewer chunks, are dispatched last
-  const int sp = blockIdx.z / p.num_seqs;  // key chunk of a split row tile
-  const int seq = blockIdx.z - sp * p.num_seqs;
-  const int h = blockIdx.y;
+  const uint3 tile = xcd_tile();
+  const int sp = tile.z / p.num_seqs;  // key chunk of a split row tile
+  const int seq = tile.z - sp * p.num_seqs;
+  const int h = tile.y;
   const int G = p.G;
   const int q_begin = p.cu[seq];
   const int S_q = p.cu[seq + 1] - q_begin;
   const int rows_total = S_q * G;
-  const int row0 = blockIdx.x * kDmaRows;
+  const int row0 = tile.x * kDmaRows;
   if (row0 >= rows_total) return;
   const int ksplit = split_keys(p);
   const int prior = p.prior[seq];
