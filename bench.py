@@ -105,26 +105,30 @@ def bench_prefill(dev, steps, warmup):
     b = W.make_prefill_batch(cfg, dev)
     K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache)
     out = torch.empty_like(b.q)
+    ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)  # split-K partials
 
     def step():
         K.paged_prefill(b.q, b.cu_seqlens, b.prior, b.max_seqlen_q, b.k_cache, b.v_cache,
-                        b.block_table, scale=cfg.head_dim ** -0.5, out=out)
+                        b.block_table, scale=cfg.head_dim ** -0.5, out=out, workspace=ws)
 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    # calls issued back to back between one event pair: the GPU time of a
+    # call (attention + merge kernels), without host gaps between calls
+    reps = 5
     times = []
-    for _ in range(steps):
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
-        step()
+        for _ in range(steps):
+            step()
         e1.record()
         torch.cuda.synchronize()
-        times.append(e0.elapsed_time(e1))
+        times.append(e0.elapsed_time(e1) / steps)
     flops = W.prefill_flops(b)
-    ms = statistics.mean(times)
-    return dict(flops=flops, ms=ms, ms_med=statistics.median(times),
-                tflops=flops / (ms * 1e-3) / 1e12)
+    ms = statistics.median(times)
+    return dict(flops=flops, ms=ms, ms_med=ms, tflops=flops / (ms * 1e-3) / 1e12)
 
 
 def cpu_baseline(gpu_batch, rows=16):
