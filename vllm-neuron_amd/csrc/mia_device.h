@@ -58,6 +58,12 @@ MIA_HD uint32_t f32_to_bf16_bits(float x) {
 
 // low / high bf16 of a packed pair -> f32 (exact).
 MIA_DEV float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+// two floats -> packed bf16 pair (round to nearest even; gfx950 v_cvt_pk_bf16_f32)
+MIA_DEV uint32_t pack2_bf16(float a, float b) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t v = {(__bf16)a, (__bf16)b};
+  return __builtin_bit_cast(uint32_t, v);
+}
 MIA_DEV float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 // f16 bits -> f32 (exact).

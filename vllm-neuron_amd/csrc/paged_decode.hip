@@ -190,24 +190,6 @@ struct KLoad<true> {
   }
 };
 
-template <bool FP8>
-MIA_DEV void v_to_f32(typename KLoad<FP8>::raw_t r, float v[8]);
-
-template <>
-MIA_DEV void v_to_f32<false>(u32x4_t r, float v[8]) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    v[2 * i] = bf16lo(r[i]);
-    v[2 * i + 1] = bf16hi(r[i]);
-  }
-}
-
-template <>
-MIA_DEV void v_to_f32<true>(u32x2_t r, float v[8]) {
-  e4m3fn_x4_to_f32_scaled(r[0], v);
-  e4m3fn_x4_to_f32_scaled(r[1], v + 4);
-}
-
 // ---------------------------------------------------------------------------
 // split kernel
 // ---------------------------------------------------------------------------
@@ -239,8 +221,10 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeKParams p) {
   using KL = KLoad<FP8>;
   using raw_t = typename KL::raw_t;
 
-  __shared__ float p_lds[kWaves][kTile][NCP];
-  __shared__ float a_lds[kWaves][16];
+  // V tile of each wave, bf16, rows of D elements, 16-byte chunks XOR-
+  // swizzled by row (chunk c of token row t at c ^ (t % (D/8))): the writes
+  // (16 lanes per row) and the transposed reads below are conflict-free
+  __shared__ __attribute__((aligned(16))) uint8_t v_lds[kWaves][kTile * D * 2];
   __shared__ int s_item0[kMaxRows + 1];
   __shared__ int s_lo[kMaxRows];
   __shared__ int s_hi[kMaxRows];
@@ -289,6 +273,37 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeKParams p) {
   const int k_lane_off = (qcol * (int)p.kc_t + kg * 8) * EB;
   const int v_lane_off = (tl * (int)p.vc_t + ds * 8) * EB;
   const int max_blk = CH / 16 + 1;  // block ids a chunk can touch (<= 64)
+
+  // ---- PV on MFMA: O^T[d, col] += V^T[d, tok] P^T[tok, col] with
+  // v_mfma_f32_16x16x32_bf16 per 16-d block.  The contraction index k of
+  // lane group g (= lane / 16) is ordered as tokens {4g..4g+3, 16+4g..16+4g+3},
+  // which are exactly the 8 scores the lane holds after QK, so P^T needs no
+  // exchange.  The V^T operand (d = 16 blk + lane % 16, those 8 tokens) is
+  // read from the wave's V tile with two ds_read_b64_tr_b16: within a 16-lane
+  // group, result lane k gets element k % 4 of the 8 bytes read by lane
+  // 4j + k/4 (j = 0..3), so source lane s addresses token row 4g + s/4 and
+  // the 4 d values at 16 blk + 4 (s % 4).
+  constexpr int VROWB = D * 2;       // bytes per V row in LDS
+  constexpr int VNCH = D / 8;        // 16-byte chunks per row
+  constexpr int DB16 = D / 16;       // 16-d MFMA blocks
+  typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
+  typedef short s16x4_t __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
+  lds_u8_t *const vw = (lds_u8_t *)&v_lds[wave][0];
+  const int tr_s = lane & 15;
+  const int tr_row = 4 * kg + (tr_s >> 2);           // token row (and + 16)
+  const int tr_x = tr_row & (VNCH - 1);              // its swizzle
+  uint32_t v_rd_off[DB16];
+#pragma unroll
+  for (int blk = 0; blk < DB16; ++blk)
+    v_rd_off[blk] = tr_row * VROWB + ((((blk * 2 + ((tr_s >> 1) & 1)) ^ tr_x)) << 4) +
+                    ((tr_s & 1) << 3);
+  // row of V load i of this lane: i * TL + tl; its swizzle repeats every
+  // VNCH / TL loads
+  auto v_wr_off = [&](int i) {
+    const int t = i * TL + tl;
+    return (uint32_t)(t * VROWB + ((ds ^ (t & (VNCH - 1))) << 4));
+  };
 
   // Item id -> (b, h, c) by binary search over the prefix sum; an id past
   // the end yields `fallback` with valid = 0 (so its loads stay in bounds).
@@ -404,11 +419,10 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeKParams p) {
     const bool wrap_q = st_cur > cur.minpos;
     float m_run = -INFINITY;  // per column (lane & 15)
     float l_run = 0.f;        // per lane partial
-    float o[NCP][8];
+    // lane holds O^T[16 blk + 4 (lane / 16) + i][column lane % 16]
+    f32x4_t oacc[DB16];
 #pragma unroll
-    for (int c = 0; c < NCP; ++c)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[c][e] = 0.f;
+    for (int blk = 0; blk < DB16; ++blk) oacc[blk] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
     const int t_first = first_tile(cur);
     for (int t0 = t_first; t0 < cur.t_hi; t0 += kTile) {
@@ -453,7 +467,23 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeKParams p) {
           sc[st][i] = ok ? sc[st][i] * scale2 : -INFINITY;
         }
       }
-      // ---- online softmax (exp2 domain)
+      // ---- V tile -> LDS (bf16; rows outside the item are zeroed: their
+      // probabilities are 0 and the clamped loads hold other rows), then
+      // the next tile's V loads
+#pragma unroll
+      for (int i = 0; i < VPL; ++i) {
+        const int tok = t0 + i * TL + tl;
+        const bool vok = tok >= cur.t_lo && tok < cur.t_hi;
+        raw_t rv = vr[i];
+#pragma unroll
+        for (int w = 0; w < (int)(sizeof(raw_t) / 4); ++w) rv[w] = vok ? rv[w] : 0u;
+        *(__attribute__((address_space(3))) u32x4_t *)(vw + v_wr_off(i)) =
+            __builtin_bit_cast(u32x4_t, KL::to_bf16(rv));
+      }
+      issue_v(vr, itN, blkN, tN);
+      // ---- online softmax (exp2 domain) with lazy rescaling: the running
+      // max only moves when the tile's max exceeds it by more than 8, so the
+      // accumulators are rescaled only on such tiles
       float mx = -INFINITY;
 #pragma unroll
       for (int st = 0; st < NSUB; ++st)
@@ -461,79 +491,53 @@ __global__ __launch_bounds__(256, 2) void decode_split_kernel(DecodeKParams p) {
         for (int i = 0; i < 4; ++i) mx = fmaxf(mx, sc[st][i]);
       mx = wave_max_xor(mx, 16);
       mx = wave_max_xor(mx, 32);
-      const float m_new = fmaxf(m_run, mx);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+      const bool bump = mx > m_run + 8.0f;
+      const float m_new = bump ? mx : m_run;
+      const float alpha = bump ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.0f;
       m_run = m_new;
+      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+      if (__builtin_amdgcn_ballot_w64(bump)) {
+#pragma unroll
+        for (int blk = 0; blk < DB16; ++blk)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) oacc[blk][i] *= alpha;
+      }
       float psum = 0.f;
+      uint32_t pk[4];
 #pragma unroll
-      for (int st = 0; st < NSUB; ++st) {
+      for (int st = 0; st < NSUB; ++st)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float pv = __builtin_amdgcn_exp2f(sc[st][i] - m_use);
-          psum += pv;
-          if (qcol < NCP) p_lds[wave][st * 16 + kg * 4 + i][qcol] = pv;
+        for (int i = 0; i < 4; i += 2) {
+          const float p0 = __builtin_amdgcn_exp2f(sc[st][i] - m_use);
+          const float p1 = __builtin_amdgcn_exp2f(sc[st][i + 1] - m_use);
+          psum += p0 + p1;
+          pk[st * 2 + (i >> 1)] = pack2_bf16(p0, p1);
         }
-      }
       l_run = l_run * alpha + psum;
-      if (lane < 16) a_lds[wave][lane] = alpha;
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-      // ---- PV on the vector ALU
-      float al[NCP];
+      const bf16x8_t bop = __builtin_bit_cast(bf16x8_t, u32x4_t{pk[0], pk[1], pk[2], pk[3]});
+      // ---- PV on MFMA
 #pragma unroll
-      for (int c = 0; c < NCP; ++c) al[c] = a_lds[wave][c];
-#pragma unroll
-      for (int c = 0; c < NCP; ++c)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[c][e] *= al[c];
-#pragma unroll
-      for (int i = 0; i < VPL; ++i) {
-        const int tloc = i * TL + tl;
-        const int tok = t0 + tloc;
-        const bool vok = tok >= cur.t_lo && tok < cur.t_hi;
-        raw_t rv = vr[i];
-#pragma unroll
-        for (int w = 0; w < (int)(sizeof(raw_t) / 4); ++w) rv[w] = vok ? rv[w] : 0u;
-        float v[8];
-        v_to_f32<FP8>(rv, v);
-        float pc[NCP];
-#pragma unroll
-        for (int c = 0; c < NCP; ++c) pc[c] = p_lds[wave][tloc][c];
-#pragma unroll
-        for (int c = 0; c < NCP; ++c)
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[c][e] = fmaf(pc[c], v[e], o[c][e]);
+      for (int blk = 0; blk < DB16; ++blk) {
+        const s16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4_t *)(vw + v_rd_off[blk]));
+        const s16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_s16x4_t *)(vw + v_rd_off[blk] + 16 * VROWB));
+        const u32x4_t aw = {__builtin_bit_cast(u32x2_t, lo)[0], __builtin_bit_cast(u32x2_t, lo)[1],
+                            __builtin_bit_cast(u32x2_t, hi)[0], __builtin_bit_cast(u32x2_t, hi)[1]};
+        oacc[blk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, aw),
+                                                            bop, oacc[blk], 0, 0, 0);
       }
-      issue_v(vr, itN, blkN, tN);
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 
     // ---- item epilogue: reduce within the wave, write the partial
     l_run = wave_sum_xor(l_run, 16);
     l_run = wave_sum_xor(l_run, 32);
-#pragma unroll
-    for (int c = 0; c < NCP; ++c)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float x = o[c][e];
-#pragma unroll
-        for (int msk = DS; msk < 64; msk <<= 1) x = wave_sum_xor(x, msk);
-        o[c][e] = x;
-      }
     const int64_t ws_row = (((int64_t)cur.b * p.Hkv + cur.h) * p.num_splits + cur.c) * p.nc_tot;
-    if (tl == 0) {
+    if (col_ok) {
+      float *dst = p.ws_o + (ws_row + gcol) * D + 4 * kg;
 #pragma unroll
-      for (int c = 0; c < NCP; ++c) {
-        if (p.col0 + c < p.nc_tot) {
-          float *dst = p.ws_o + (ws_row + p.col0 + c) * D + ds * 8;
-          *reinterpret_cast<f32x4_t *>(dst) = f32x4_t{o[c][0], o[c][1], o[c][2], o[c][3]};
-          *reinterpret_cast<f32x4_t *>(dst + 4) = f32x4_t{o[c][4], o[c][5], o[c][6], o[c][7]};
-        }
-      }
+      for (int blk = 0; blk < DB16; ++blk)
+        *reinterpret_cast<f32x4_t *>(dst + blk * 16) = oacc[blk];
     }
     if (lane < NCP && p.col0 + lane < p.nc_tot) {
       p.ws_ml[(ws_row + p.col0 + lane) * 2] = m_run;

@@ -79,12 +79,6 @@ struct PrefillKParams {
   int rows_max;   // max_seqlen_q * G
 };
 
-MIA_DEV uint32_t pack2_bf16(float a, float b) {
-  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
-  const bf16x2_t v = {(__bf16)a, (__bf16)b};  // round to nearest even
-  return __builtin_bit_cast(uint32_t, v);
-}
-
 // Key range of the workgroup whose rows start at row0 (rows are GQA-packed:
 // row = pos * G + g): tiles kt0 .. kt_last (64-key aligned) and the number
 // of key chunks it spans.  Shared by the attention and combine kernels so
