@@ -130,6 +130,21 @@ MIA_DEV void e4m3fn_x4_to_f32_scaled(uint32_t w, float out[4]) {
   out[3] = f16_bits_to_f32(hi >> 16);
 }
 
+// 8 e4m3fn bytes (two dwords, byte order = element order) -> 8 bf16 values
+// x * 2^-8 (exact in bf16), with the gfx950 scaled conversion
+// v_cvt_scalef32_pk_bf16_fp8 (two values per instruction; word select 0
+// takes bytes 0-1, 1 takes bytes 2-3).  Same values as
+// e4m3fn_x4_to_f32_scaled for every non-NaN code.
+MIA_DEV u32x4_t e4m3fn_x8_to_bf16_scaled(u32x2_t r) {
+  constexpr float kS = 0.00390625f;  // 2^-8
+  u32x4_t w;
+  w[0] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r[0], kS, false));
+  w[1] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r[0], kS, true));
+  w[2] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r[1], kS, false));
+  w[3] = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(r[1], kS, true));
+  return w;
+}
+
 // Quantise one value the way the reference writes an FP8 cache.
 //   MIA_QUANT_MUL_BF16: bf16(x * s) (x, s bf16-exact), clamp +-448, e4m3fn
 //   MIA_QUANT_MUL_F32 : f32(x * s), clamp, e4m3fn

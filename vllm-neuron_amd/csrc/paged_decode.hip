@@ -181,17 +181,9 @@ struct KLoad<true> {
     return *reinterpret_cast<const u32x2_t *>(p);
   }
   static MIA_DEV raw_t zero() { return raw_t{0u, 0u}; }
-  // values are x * 2^-8 (see e4m3fn_x4_to_f32_scaled); exact in bf16.
+  // values are x * 2^-8, exact in bf16
   static MIA_DEV bf16x8_t to_bf16(raw_t r) {
-    float f[8];
-    e4m3fn_x4_to_f32_scaled(r[0], f);
-    e4m3fn_x4_to_f32_scaled(r[1], f + 4);
-    u32x4_t w;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      w[i] = (__float_as_uint(f[2 * i]) >> 16) |
-             (__float_as_uint(f[2 * i + 1]) & 0xffff0000u);
-    return __builtin_bit_cast(bf16x8_t, w);
+    return __builtin_bit_cast(bf16x8_t, e4m3fn_x8_to_bf16_scaled(r));
   }
 };
 

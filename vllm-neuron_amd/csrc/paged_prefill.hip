@@ -216,16 +216,7 @@ template <>
 struct Chunk8<true> {
   typedef u32x2_t raw_t;
   static MIA_DEV raw_t load(const uint8_t *p) { return *reinterpret_cast<const u32x2_t *>(p); }
-  static MIA_DEV u32x4_t bf16(raw_t r) {
-    float f[8];
-    e4m3fn_x4_to_f32_scaled(r[0], f);
-    e4m3fn_x4_to_f32_scaled(r[1], f + 4);
-    u32x4_t w;
-#pragma unroll
-    for (int i = 0; i < 4; ++i)
-      w[i] = (__float_as_uint(f[2 * i]) >> 16) | (__float_as_uint(f[2 * i + 1]) & 0xffff0000u);
-    return w;
-  }
+  static MIA_DEV u32x4_t bf16(raw_t r) { return e4m3fn_x8_to_bf16_scaled(r); }
 };
 
 
