@@ -259,3 +259,31 @@ def test_fused_cache_write_matches_scatter(gpu, case, S):
     torch.cuda.synchronize()
     assert torch.equal(b.k_cache.view(torch.uint8), kc.view(torch.uint8))
     assert torch.equal(b.v_cache.view(torch.uint8), vc.view(torch.uint8))
+
+
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_fp8_cache_codes_widen_exactly(gpu, head_dim):
+    """Every e4m3fn code (NaN codes replaced by 0) of a visible prior V row
+    comes out exactly: one prior key with probability 1 (the active key's
+    score is far below, so its probability underflows to 0), dequant scales
+    1.0, so the output row is the FP8 value itself, exact in bf16."""
+    d = head_dim
+    rows = 256 // d
+    cfg = _small_cfg(batch=rows, q_heads=1, kv_heads=1, head_dim=d, block_size=16,
+                     ctx_lo=2, ctx_hi=2, fp8=True)
+    b = W.make_decode_batch(cfg, gpu)
+    codes = torch.arange(256, dtype=torch.int32)
+    codes[(codes & 0x7F) == 0x7F] = 0                      # e4m3fn NaN codes
+    codes = codes.to(torch.uint8).view(rows, d)
+    one = torch.ones(1, dtype=torch.float32, device=gpu)
+    b.k_dequant, b.v_dequant, b.k_quant, b.v_quant = one, one.clone(), one.clone(), one.clone()
+    kc, vc = b.k_cache.view(torch.uint8), b.v_cache.view(torch.uint8)
+    for r in range(rows):
+        phys = int(b.block_table[r, 0])
+        kc[phys, 0, 0].zero_()                             # prior key: score 0
+        vc[phys, 0, 0] = codes[r].to(gpu)
+    b.q = torch.ones_like(b.q)
+    b.k_new = torch.full_like(b.k_new, -448.0)             # active key: score -> -inf
+    out = _run_core(b).float().cpu().view(rows, d)
+    want = codes.view(torch.float8_e4m3fn).float().to(torch.bfloat16).float()
+    assert torch.equal(out, want)
