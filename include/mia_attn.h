@@ -309,6 +309,27 @@ typedef struct {
   size_t workspace_bytes;
   int32_t split_tokens;
   int32_t _pad0;
+  /* Generalised visibility for dense attention (attention_cte.py:47-186,
+   * flash_attention :189-343); all zero / NULL keeps the rule above.
+   *   kv_len      device [num_seqs]: keys [0, kv_len) exist (NULL: prior + S_q).
+   *   non_causal  every existing key is visible (no causal or window limit).
+   *   q_offset    added to every query position (the context-parallel offset:
+   *               query row r of sequence i sits at prior + r + q_offset).
+   *   bound_min / bound_max  device int32 per (query token t, q head hq) at
+   *               bound_stride[0] * t + bound_stride[1] * hq (both or neither):
+   *               key k is visible only if bound_min <= k < bound_max.
+   *   empty_rows_uniform  a row that sees no key and has no sink attends to
+   *               all kv_len keys with equal weight (the dense reference masks
+   *               scores with the dtype's lowest value, not -inf); otherwise
+   *               (and always with a sink) such a row outputs 0. */
+  const int32_t *kv_len;
+  const int32_t *bound_min;
+  const int32_t *bound_max;
+  int64_t bound_stride[2];
+  int32_t non_causal;
+  int32_t q_offset;
+  int32_t empty_rows_uniform;
+  int32_t _pad3;
 } mia_prefill_args;
 
 size_t mia_prefill_workspace_bytes(const mia_prefill_args *args);

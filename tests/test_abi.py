@@ -91,6 +91,39 @@ def test_decode_validation(over, err, text):
         N.check(rc, "paged_decode")
 
 
+def _prefill_args(**over):
+    a = N.PrefillArgs()
+    fake = 0x10000  # never dereferenced: validation fails first
+    for f in ("q", "cu_seqlens_q", "prior_tokens", "k_cache", "v_cache", "block_table", "out"):
+        setattr(a, f, fake)
+    a.q_stride = (ctypes.c_int64 * 3)(1024, 128, 1)
+    a.num_seqs, a.max_seqlen_q, a.num_tokens = 1, 4, 4
+    a.cache_dtype = N.DTYPE_BF16
+    a.k_cache_stride = (ctypes.c_int64 * 5)(16384, 8192, 128, 1, 0)
+    a.v_cache_stride = (ctypes.c_int64 * 4)(16384, 8192, 128, 1)
+    a.num_blocks, a.block_size, a.blocks_per_seq = 4, 64, 2
+    a.num_q_heads, a.num_kv_heads, a.head_dim = 8, 2, 128
+    a.out_dtype = N.DTYPE_BF16
+    a.out_stride = (ctypes.c_int64 * 3)(1024, 128, 1)
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("over,text", [
+    (dict(bound_min=0x10000), "both"),
+    (dict(bound_max=0x10000), "both"),
+    (dict(bound_min=0x10000, bound_max=0x10000,
+          bound_stride=(ctypes.c_int64 * 2)(-1, 4)), "negative bound"),
+])
+def test_prefill_bounds_validation(over, text):
+    a = _prefill_args(**over)
+    L = N.lib()
+    assert L.mia_prefill_workspace_bytes(ctypes.byref(a)) == 0
+    with pytest.raises(ValueError, match=text):
+        N.check(L.mia_paged_prefill(ctypes.byref(a), None), "paged_prefill")
+
+
 def test_null_args_are_value_errors():
     L = N.lib()
     for fn in (L.mia_paged_decode, L.mia_paged_prefill, L.mia_kv_write, L.mia_gather_kv,

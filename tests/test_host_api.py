@@ -15,6 +15,7 @@ import torch
 
 from vllm_neuron_amd import _native as N
 from vllm_neuron_amd import workloads as W
+from vllm_neuron_amd.functional.attention.attention_cte import flash_attention
 from vllm_neuron_amd.functional.attention.attention_decode import attention_decode
 from vllm_neuron_amd.functional.attention.attention_decode_mask import gen_attention_decode_mask
 from vllm_neuron_amd.functional.attention.attention_segmented_cte import segmented_attention
@@ -42,6 +43,28 @@ def test_mask_and_prefill_refuse_cpu_tensors():
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         segmented_attention(q, kc, kc.clone(), torch.ones(1, 4, dtype=torch.int32),
                             torch.tensor([0]), 16, 64, 0.125)
+
+
+def test_flash_attention_argument_contract():
+    """CPU tensors are refused (no fallback); unsupported options raise
+    before any device work."""
+    q = torch.randn(4, 16, 64).to(torch.bfloat16)
+    k = torch.randn(2, 64, 16).to(torch.bfloat16)
+    v = torch.randn(2, 16, 64).to(torch.bfloat16)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        flash_attention(q, k, v)
+    with pytest.raises(NotImplementedError):
+        flash_attention(q, k, v, global_cp_deg=2, cp_offset=torch.zeros(1, 1))
+    with pytest.raises(ValueError):
+        flash_attention(q, k, v, bound_min=torch.zeros(4, 16, 1, dtype=torch.int32))
+    with pytest.raises(ValueError):
+        flash_attention(q[:3], k, v)                       # 3 % 2 != 0
+    with pytest.raises(NotImplementedError):
+        flash_attention(q.float(), k.float(), v.float())
+    with pytest.raises(NotImplementedError):
+        flash_attention(torch.zeros(4, 16, 160, dtype=torch.bfloat16),
+                        torch.zeros(2, 160, 16, dtype=torch.bfloat16),
+                        torch.zeros(2, 16, 160, dtype=torch.bfloat16))
 
 
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):

@@ -243,6 +243,10 @@ static int validate_prefill(const mia_prefill_args *a) {
               MIA_ERR_VALUE, "prefill: output must be bf16 with contiguous d");
   MIA_REQUIRE(a->max_seqlen_q >= 0, MIA_ERR_VALUE, "prefill: max_seqlen_q < 0");
   MIA_REQUIRE(a->split_tokens >= 0, MIA_ERR_VALUE, "prefill: negative split_tokens");
+  MIA_REQUIRE((a->bound_min == nullptr) == (a->bound_max == nullptr), MIA_ERR_VALUE,
+              "prefill: bound_min and bound_max must both be set or both be NULL");
+  MIA_REQUIRE(a->bound_stride[0] >= 0 && a->bound_stride[1] >= 0, MIA_ERR_VALUE,
+              "prefill: negative bound strides");
   return MIA_OK;
 }
 

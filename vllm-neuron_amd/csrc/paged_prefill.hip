@@ -77,6 +77,13 @@ struct PrefillKParams {
   int slots;      // workgroups resident on the device at once
   int rows_wg;    // query rows per workgroup of the attention kernel
   int rows_max;   // max_seqlen_q * G
+  // generalised visibility (dense attention); all zero = segmented rule
+  const int32_t *kv_len;          // [num_seqs] keys per sequence (NULL: prior + S_q)
+  const int32_t *bmin, *bmax;     // per (token, q head) key bounds or NULL
+  int64_t b_st, b_sh;
+  int non_causal;                 // every existing key visible
+  int q_off;                      // added to query positions
+  int uniform;                    // empty rows (no sink) attend uniformly
 };
 
 // Key range of the workgroup whose rows start at row0 (rows are GQA-packed:
@@ -85,19 +92,85 @@ struct PrefillKParams {
 // that both agree on which rows were split.
 struct KeyRange {
   int kmin, kmax;       // keys visible to some row
+  int full_lo, full_hi; // keys visible to every row: [full_lo, full_hi)
   int kt0, kt_last;     // first / last tile
   int n_sp;             // chunks of ksplit keys covering the tiles
   bool any;
 };
 
-MIA_DEV KeyRange wg_key_range(const PrefillKParams &p, int prior, int S_q, int row0,
+// Keys that exist for sequence seq: [0, kv_len) (segmented rule: prior +
+// S_q), never past the block table.
+MIA_DEV int seq_kv_len(const PrefillKParams &p, int seq, int prior, int S_q) {
+  return min(p.kv_len ? p.kv_len[seq] : prior + S_q, p.nblk * p.bs);
+}
+
+// Visible keys [lo, hi) of the query at position pos (token tok, q head hq)
+// of a sequence with `prior` earlier tokens and kvl keys.  Causal: the
+// query's absolute position qp = prior + pos + q_off sees k <= qp and, with
+// a window, k > qp - window; non-causal: every key.  Bounds narrow the range
+// further.  Returns true for a row that, having no visible key, attends to
+// all kvl keys uniformly (the dense rule without sink): its range is then
+// [0, kvl) and the caller zeroes its query so every score is 0.
+MIA_DEV bool row_range(const PrefillKParams &p, int prior, int kvl, int pos, int64_t tok, int hq,
+                       bool row_ok, int &lo, int &hi) {
+  const int qp = prior + pos + p.q_off;
+  if (p.non_causal) {
+    lo = 0;
+    hi = kvl;
+  } else {
+    hi = min(qp + 1, kvl);
+    lo = p.window > 0 ? qp - p.window + 1 : 0;
+  }
+  if (p.bmin && row_ok) {
+    const int64_t bi = tok * p.b_st + (int64_t)hq * p.b_sh;
+    lo = max(lo, p.bmin[bi]);
+    hi = min(hi, p.bmax[bi]);
+  }
+  const bool uni = p.uniform && !p.sink && row_ok && max(lo, 0) >= hi && kvl > 0;
+  if (uni) {
+    lo = 0;
+    hi = kvl;
+  }
+  return uni;
+}
+
+// Key range of the workgroup whose rows start at row0 (rows are GQA-packed:
+// row = pos * G + g): the keys some row sees, the keys every row sees, the
+// tiles and the number of key chunks.  Shared by the attention and merge
+// kernels so that all agree on which rows were split.
+MIA_DEV KeyRange wg_key_range(const PrefillKParams &p, int seq, int prior, int S_q, int row0,
                               int ksplit) {
   KeyRange k;
-  const int s_ctx = p.nblk * p.bs;
+  const int kvl = seq_kv_len(p, seq, prior, S_q);
   const int pos_lo = row0 / p.G;
   const int pos_hi = min(S_q - 1, (row0 + p.rows_wg - 1) / p.G);
-  k.kmax = min(min(prior + pos_hi + 1, prior + S_q), s_ctx);
-  k.kmin = p.window > 0 ? max(0, prior + pos_lo - p.window + 1) : 0;
+  bool wide = p.bmin != nullptr;  // rows may see any subset of [0, kvl)
+  if (p.non_causal) {
+    k.kmin = 0;
+    k.kmax = kvl;
+    k.full_lo = 0;
+    k.full_hi = kvl;
+  } else {
+    // causal rows are monotone in the position: the extreme rows decide
+    const int q_lo = prior + pos_lo + p.q_off, q_hi = prior + pos_hi + p.q_off;
+    k.kmax = min(q_hi + 1, kvl);
+    k.kmin = p.window > 0 ? max(0, q_lo - p.window + 1) : 0;
+    k.full_hi = min(q_lo + 1, kvl);
+    k.full_lo = p.window > 0 ? q_hi - p.window + 1 : 0;
+    if (p.uniform && !p.sink) {
+      // an empty causal row lies at an end of the position range
+      auto empty = [&](int qp) {
+        return min(qp + 1, kvl) <= (p.window > 0 ? max(qp - p.window + 1, 0) : 0);
+      };
+      wide = wide || empty(q_lo) || empty(q_hi);
+    }
+  }
+  if (wide) {
+    k.kmin = 0;
+    k.kmax = kvl;
+    k.full_lo = 1 << 30;  // no tile is seen by every row
+    k.full_hi = -(1 << 30);
+  }
   k.any = k.kmax > k.kmin;
   k.kt0 = (k.kmin / kKT) * kKT;
   k.kt_last = k.kmax > k.kt0 ? ((k.kmax - 1) / kKT) * kKT : k.kt0;
@@ -255,7 +328,6 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
   const int lane = tid & 63;
   const int half = lane >> 5;   // k-group of MFMA operands
   const int rl = lane & 31;     // row (B operand column) of this lane
-  const int s_ctx = p.nblk * p.bs;
 
   // ---- this lane's query row
   const int r = row0 + wave * kRowsW + rl;
@@ -263,19 +335,18 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
   const int g_r = r - pos_r * G;
   const bool row_ok = r < rows_total && q_begin + pos_r < p.num_tokens;
   const int hq = h * G + g_r;
-  const int r_hi = min(min(prior + pos_r + 1, prior + S_q), s_ctx);  // k < r_hi
-  const int r_lo = p.window > 0 ? prior + pos_r - p.window + 1 : 0;  // k >= r_lo
+  int r_lo, r_hi;  // this row sees keys [r_lo, r_hi)
+  const bool uni = row_range(p, prior, seq_kv_len(p, seq, prior, S_q), pos_r,
+                             (int64_t)q_begin + pos_r, hq, row_ok, r_lo, r_hi);
 
   // ---- workgroup key range and the all-visible range
-  const int pos_lo = row0 / G;
-  const int pos_hi = min(S_q - 1, (row0 + kRowsWG - 1) / G);
-  const int kmax = min(min(prior + pos_hi + 1, prior + S_q), s_ctx);
-  const int kmin = p.window > 0 ? max(0, prior + pos_lo - p.window + 1) : 0;
-  const int full_hi = min(min(prior + pos_lo + 1, prior + S_q), s_ctx);  // every row sees k < full_hi
-  const int full_lo = p.window > 0 ? prior + pos_hi - p.window + 1 : 0;  // and k >= full_lo
+  const KeyRange kr = wg_key_range(p, seq, prior, S_q, row0, ksplit);
+  const int kmax = kr.kmax;
+  const int full_hi = kr.full_hi;  // every row sees k < full_hi
+  const int full_lo = kr.full_lo;  // and k >= full_lo
   // no visible key for any row (a table shorter than the window start):
   // no tile is loaded and every row outputs 0
-  const bool any_key = kmax > kmin;
+  const bool any_key = kr.any;
 
   // ---- Q^T fragments (B operand): lane holds Q[row rl][ks*16 + half*8 .. +8]
   bf16x8_t qf[KSTEPS];
@@ -284,8 +355,8 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
                          (int64_t)(row_ok ? hq : 0) * p.qs_h;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
-      u32x4_t w = {0u, 0u, 0u, 0u};
-      if (row_ok) w = *reinterpret_cast<const u32x4_t *>(qp + ks * 16 + half * 8);
+      u32x4_t w = {0u, 0u, 0u, 0u};  // zero query: uniform row, scores 0
+      if (row_ok && !uni) w = *reinterpret_cast<const u32x4_t *>(qp + ks * 16 + half * 8);
       qf[ks] = __builtin_bit_cast(bf16x8_t, w);
     }
   }
@@ -304,7 +375,6 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
   // (chunk c of 4 keys goes to slot [0, 2, 1, 3][c]) to match the P^T layout
   const int v_col = (vg >> 2) * 16 + (((vg & 1) << 1) | ((vg >> 1) & 1)) * 4;
 
-  const KeyRange kr = wg_key_range(p, prior, S_q, row0, ksplit);
   if (sp >= kr.n_sp) return;  // no chunk for this workgroup
   int kt0 = kr.kt0, kt_last = kr.kt_last;
   if (kr.n_sp > 1) {
@@ -506,7 +576,6 @@ __global__ __launch_bounds__(512, 1) void prefill_dma_kernel(PrefillKParams p) {
   typedef short s16x4_t __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
   typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
-  typedef __attribute__((address_space(3))) void lds_void_t;
 
   __shared__ int32_t ids_lds[kDmaIds];
   __shared__ __attribute__((aligned(1024))) uint8_t kv_lds[3][2][TILEB];  // [stage][K, V]
@@ -534,24 +603,20 @@ __global__ __launch_bounds__(512, 1) void prefill_dma_kernel(PrefillKParams p) {
   const int lane = tid & 63;
   const int half = lane >> 5;
   const int rl = lane & 31;
-  const int s_ctx = p.nblk * p.bs;
 
   const int r = row0 + wave * kRowsW + rl;
   const int pos_r = r / G;
   const int g_r = r - pos_r * G;
   const bool row_ok = r < rows_total && q_begin + pos_r < p.num_tokens;
   const int hq = h * G + g_r;
-  const int r_hi = min(min(prior + pos_r + 1, prior + S_q), s_ctx);
-  const int r_lo = p.window > 0 ? prior + pos_r - p.window + 1 : 0;
+  int r_lo, r_hi;  // this row sees keys [r_lo, r_hi)
+  const bool uni = row_range(p, prior, seq_kv_len(p, seq, prior, S_q), pos_r,
+                             (int64_t)q_begin + pos_r, hq, row_ok, r_lo, r_hi);
 
-  const int pos_lo = row0 / G;
-  const int pos_hi = min(S_q - 1, (row0 + kDmaRows - 1) / G);
-  const int kmax = min(min(prior + pos_hi + 1, prior + S_q), s_ctx);
-  const int kmin = p.window > 0 ? max(0, prior + pos_lo - p.window + 1) : 0;
-  const int full_hi = min(min(prior + pos_lo + 1, prior + S_q), s_ctx);
-  const int full_lo = p.window > 0 ? prior + pos_hi - p.window + 1 : 0;
-  const bool any_key = kmax > kmin;
-  const KeyRange kr = wg_key_range(p, prior, S_q, row0, ksplit);
+  const KeyRange kr = wg_key_range(p, seq, prior, S_q, row0, ksplit);
+  const int full_hi = kr.full_hi;
+  const int full_lo = kr.full_lo;
+  const bool any_key = kr.any;
   if (sp >= kr.n_sp) return;  // no chunk for this workgroup
   int kt0 = kr.kt0, kt_last = kr.kt_last;
   if (kr.n_sp > 1) {
@@ -566,8 +631,8 @@ __global__ __launch_bounds__(512, 1) void prefill_dma_kernel(PrefillKParams p) {
                          (int64_t)(row_ok ? hq : 0) * p.qs_h;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
-      u32x4_t w = {0u, 0u, 0u, 0u};
-      if (row_ok) w = *reinterpret_cast<const u32x4_t *>(qp + ks * 16 + half * 8);
+      u32x4_t w = {0u, 0u, 0u, 0u};  // zero query: uniform row, scores 0
+      if (row_ok && !uni) w = *reinterpret_cast<const u32x4_t *>(qp + ks * 16 + half * 8);
       qf[ks] = __builtin_bit_cast(bf16x8_t, w);
     }
     // wait for Q here, before the copy ring starts: a wait placed by the
@@ -799,7 +864,7 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillKParams p) 
   const int r0 = blockIdx.x * 16;  // inside one row tile (rows_wg % 16 == 0)
   if (r0 >= rows_total) return;
   const KeyRange kr =
-      wg_key_range(p, p.prior[seq], S_q, (r0 / p.rows_wg) * p.rows_wg, split_keys(p));
+      wg_key_range(p, seq, p.prior[seq], S_q, (r0 / p.rows_wg) * p.rows_wg, split_keys(p));
   if (kr.n_sp <= 1) return;
   const int n_sp = min(kr.n_sp, kMaxSp);
   const int lane = threadIdx.x & 63;
@@ -963,6 +1028,14 @@ int launch_paged_prefill(const mia_prefill_args &a, const PrefillPlan &pl, hipSt
   kp.num_seqs = a.num_seqs;
   kp.rows_wg = pl.rows_wg;
   kp.rows_max = pl.rows_max;
+  kp.kv_len = a.kv_len;
+  kp.bmin = a.bound_min;
+  kp.bmax = a.bound_max;
+  kp.b_st = a.bound_stride[0];
+  kp.b_sh = a.bound_stride[1];
+  kp.non_causal = a.non_causal ? 1 : 0;
+  kp.q_off = a.q_offset;
+  kp.uniform = a.empty_rows_uniform ? 1 : 0;
   const dim3 grid((unsigned)((pl.rows_max + pl.rows_wg - 1) / pl.rows_wg),
                   (unsigned)a.num_kv_heads, (unsigned)(pl.nsplit * a.num_seqs));
   if (pl.dma) {

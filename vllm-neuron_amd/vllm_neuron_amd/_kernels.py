@@ -392,13 +392,26 @@ def paged_prefill(
     out: Optional[torch.Tensor] = None,
     split_tokens: int = 0,
     workspace: Optional[torch.Tensor] = None,
+    kv_len: Optional[torch.Tensor] = None,
+    non_causal: bool = False,
+    q_offset: int = 0,
+    bound_min: Optional[torch.Tensor] = None,
+    bound_max: Optional[torch.Tensor] = None,
+    empty_rows_uniform: bool = False,
 ) -> torch.Tensor:
     """``q [T, Hq, d]`` (any token/head strides) over paged K/V; sequence i
     owns rows ``cu_seqlens_q[i]:cu_seqlens_q[i+1]`` and table row i.
 
     Long key ranges are split into chunks of ``split_tokens`` keys (0: chosen
     from the shapes) whose partials are merged by a second kernel; the
-    partials live in ``workspace`` (allocated here when not given)."""
+    partials live in ``workspace`` (allocated here when not given).
+
+    Dense-attention options (all off = the segmented rule): ``kv_len``
+    ``[num_seqs]`` keys per sequence (default prior + S_q), ``non_causal``,
+    ``q_offset`` added to query positions, per-(token, q head) key bounds
+    ``bound_min``/``bound_max`` ``[T, Hq]`` (int32, any strides; key k is
+    visible iff bound_min <= k < bound_max), and ``empty_rows_uniform``
+    (a row that sees no key and has no sink averages all keys uniformly)."""
     dev = N.require_gpu(q, cu_seqlens_q, prior_tokens, k_cache, v_cache, block_table)
     if q.dtype != torch.bfloat16:
         raise NotImplementedError("prefill: q must be bf16")
@@ -466,6 +479,28 @@ def paged_prefill(
     a.out = out.data_ptr()
     a.out_stride = _arr(ctypes.c_int64, list(out.stride()))
     a.split_tokens = int(split_tokens)
+    kvl = None
+    if kv_len is not None:
+        kvl = kv_len.reshape(-1).to(device=dev, dtype=torch.int32).contiguous()
+        if kvl.numel() < num_seqs:
+            raise ValueError("kv_len shorter than the number of sequences")
+        a.kv_len = kvl.data_ptr()
+    if (bound_min is None) != (bound_max is None):
+        raise ValueError("bound_min and bound_max must both be given or both be None")
+    bmin = bmax = None
+    if bound_min is not None:
+        bmin = bound_min.to(device=dev, dtype=torch.int32)
+        bmax = bound_max.to(device=dev, dtype=torch.int32)
+        if tuple(bmin.shape) != (T, Hq) or tuple(bmax.shape) != (T, Hq):
+            raise ValueError(f"bounds must be [T, Hq] = [{T}, {Hq}]")
+        if bmin.stride() != bmax.stride():
+            bmin, bmax = bmin.contiguous(), bmax.contiguous()
+        a.bound_min = bmin.data_ptr()
+        a.bound_max = bmax.data_ptr()
+        a.bound_stride = _arr(ctypes.c_int64, list(bmin.stride()))
+    a.non_causal = 1 if non_causal else 0
+    a.q_offset = int(q_offset)
+    a.empty_rows_uniform = 1 if empty_rows_uniform else 0
     L = N.lib()
     need = L.mia_prefill_workspace_bytes(ctypes.byref(a))
     if need:
