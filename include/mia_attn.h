@@ -78,7 +78,8 @@ int mia_abi_version(void);
 const char *mia_last_error(void);
 /* sizeof() of each argument struct, so bindings can check their layout.
  * which: 0 kv_write, 1 gather, 2 mask, 3 decode, 4 prefill, 5 slot_mapping,
- * 6 packed_k, 7 swa_trim, 8 scatter_rows.  Returns 0 for an unknown index. */
+ * 6 packed_k, 7 swa_trim, 8 scatter_rows, 9 stage.  Returns 0 for an unknown
+ * index. */
 size_t mia_args_size(int which);
 
 /* ------------------------------------------------------------------------ */
@@ -436,6 +437,35 @@ typedef struct {
 } mia_scatter_rows_args;
 
 int mia_scatter_rows(const mia_scatter_rows_args *args, mia_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Dense attention staging                                                   */
+/* Replaces: attention_cte.py:96-118 (torch.cat of the first prior_used_len */
+/*           rows of k_prior / v_prior before the new rows) and the layout  */
+/*           transposes of :80-94, feeding the prefill kernels.             */
+/* dst[h, t, e] (bf16, d contiguous) for t < out_rows, e < out_dim:          */
+/*   prior[h, t, e]      t < prior_rows, e < head_dim                        */
+/*   src[h, t - P, e]    P <= t < P + rows, e < head_dim   (P = prior_rows)  */
+/*   0                   otherwise (tail rows and padded head dims)          */
+/* src and prior are bf16 with any element strides (head, row, d): a d-major */
+/* [H, D, S] tensor is read through strides (D*S, 1, S).                     */
+/* ------------------------------------------------------------------------ */
+typedef struct {
+  const void *src;
+  int64_t src_stride[3];   /* elements: head, row, d */
+  const void *prior;       /* may be NULL when prior_rows == 0 */
+  int64_t prior_stride[3];
+  void *dst;               /* 16-byte aligned */
+  int64_t dst_stride[2];   /* elements: head, row (multiples of 8) */
+  int32_t num_heads;
+  int32_t rows;
+  int32_t prior_rows;
+  int32_t out_rows;        /* >= prior_rows + rows */
+  int32_t head_dim;
+  int32_t out_dim;         /* multiple of 8, head_dim <= out_dim <= 128 */
+} mia_stage_args;
+
+int mia_stage_rows(const mia_stage_args *args, mia_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -124,11 +124,31 @@ def test_prefill_bounds_validation(over, text):
         N.check(L.mia_paged_prefill(ctypes.byref(a), None), "paged_prefill")
 
 
+@pytest.mark.parametrize("over,text", [
+    (dict(out_dim=100), "multiple of 8"),
+    (dict(head_dim=136, out_dim=136), "multiple of 8"),
+    (dict(out_rows=10), "row counts"),
+    (dict(dst=0x10008), "aligned"),
+    (dict(src=None), "null src"),
+    (dict(prior_rows=4, out_rows=64), "null prior"),
+])
+def test_stage_validation(over, text):
+    a = N.StageArgs()
+    a.src = a.dst = 0x10000  # never dereferenced: validation fails first
+    a.src_stride = (ctypes.c_int64 * 3)(6400, 64, 1)
+    a.dst_stride = (ctypes.c_int64 * 2)(8192, 128)
+    a.num_heads, a.rows, a.out_rows, a.head_dim, a.out_dim = 2, 50, 64, 64, 128
+    for k, v in over.items():
+        setattr(a, k, v)
+    with pytest.raises(ValueError, match=text):
+        N.check(N.lib().mia_stage_rows(ctypes.byref(a), None), "stage_rows")
+
+
 def test_null_args_are_value_errors():
     L = N.lib()
     for fn in (L.mia_paged_decode, L.mia_paged_prefill, L.mia_kv_write, L.mia_gather_kv,
                L.mia_decode_mask, L.mia_slot_mapping, L.mia_swa_trim, L.mia_packed_k_convert,
-               L.mia_scatter_rows):
+               L.mia_scatter_rows, L.mia_stage_rows):
         rc = fn(None, None)
         assert rc == N.MIA_ERR_VALUE, fn.__name__
         assert L.mia_last_error()  # a message was recorded

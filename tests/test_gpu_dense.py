@@ -29,6 +29,8 @@ CASES = [
     (4, 2, 333, 333, 32, False, 0, 0, False, None, False, True, True, 0),
     (6, 3, 70, 70, 128, True, 16, 100, True, 7, True, True, False, 0),
     (2, 1, 1, 1, 128, True, 0, 0, False, None, True, False, False, 0),
+    (4, 2, 128, 256, 128, False, 0, 0, False, None, True, True, False, 0),  # K, V, q in place
+    (4, 2, 64, 192, 64, True, 0, 0, True, None, True, True, True, 128),
 ]
 
 
@@ -173,3 +175,26 @@ def test_one_sided_bounds_rejected(gpu):
     b = torch.zeros(4, 2, dtype=torch.int32, device=gpu)
     with pytest.raises(ValueError):
         K.paged_prefill(q, cu, prior, 4, kc, kc, table, scale=1.0, bound_min=b)
+
+
+@pytest.mark.parametrize("H,S,P,extra,D,Dp,layout", [
+    (2, 100, 0, 28, 80, 128, "rows"),       # tail rows, padded d
+    (3, 256, 0, 0, 128, 128, "dmajor"),     # transposed source
+    (2, 70, 37, 21, 64, 64, "dmajor"),      # prior rows (token-major) before d-major rows
+    (1, 5, 3, 0, 8, 8, "rows"),
+    (4, 0, 64, 0, 128, 128, "rows"),        # prior only
+])
+def test_stage_rows_exact(gpu, H, S, P, extra, D, Dp, layout):
+    """Staging is a pure copy: bit-exact against concatenation and padding."""
+    g = torch.Generator().manual_seed(S + P)
+    rows = torch.randn(H, S, D, generator=g).to(torch.bfloat16)
+    prior = torch.randn(H, P + 5, D, generator=g).to(torch.bfloat16)
+    Lp = P + S + extra
+    exp = torch.zeros(H, Lp, Dp, dtype=torch.bfloat16)
+    exp[:, :P, :D] = prior[:, :P]
+    exp[:, P:P + S, :D] = rows
+    src = rows.to(gpu)
+    if layout == "dmajor":
+        src = rows.transpose(1, 2).contiguous().to(gpu).transpose(1, 2)
+    got = K.stage_rows(src, prior.to(gpu) if P else None, P, Lp, Dp)
+    assert torch.equal(got.cpu(), exp)

@@ -54,6 +54,7 @@ size_t mia_args_size(int which) {
     case 6: return sizeof(mia_packed_k_args);
     case 7: return sizeof(mia_swa_trim_args);
     case 8: return sizeof(mia_scatter_rows_args);
+    case 9: return sizeof(mia_stage_args);
     default: return 0;
   }
 }
@@ -271,6 +272,26 @@ int mia_paged_prefill(const mia_prefill_args *a, mia_stream_t stream) {
                 "prefill: workspace must be 16-byte aligned");
   }
   return mia::launch_paged_prefill(*a, pl, (hipStream_t)stream);
+}
+
+int mia_stage_rows(const mia_stage_args *a, mia_stream_t stream) {
+  mia::g_last_error.clear();
+  MIA_REQUIRE(a, MIA_ERR_VALUE, "stage: null args");
+  MIA_REQUIRE(a->num_heads >= 0 && a->num_heads <= 65535 && a->rows >= 0 &&
+                  a->prior_rows >= 0 && a->out_rows >= 0 &&
+                  (int64_t)a->prior_rows + a->rows <= a->out_rows,
+              MIA_ERR_VALUE, "stage: bad row counts");
+  MIA_REQUIRE(a->out_dim > 0 && a->out_dim % 8 == 0 && a->out_dim <= 128 && a->head_dim >= 0 &&
+                  a->head_dim <= a->out_dim,
+              MIA_ERR_VALUE, "stage: out_dim must be a multiple of 8 in [head_dim, 128]");
+  if (a->num_heads == 0 || a->out_rows == 0) return MIA_OK;
+  MIA_REQUIRE(a->dst && aligned(a->dst, 16) && a->dst_stride[0] % 8 == 0 &&
+                  a->dst_stride[1] % 8 == 0 && a->dst_stride[1] >= a->out_dim,
+              MIA_ERR_VALUE, "stage: dst must be 16-byte aligned with row strides of 8 elements");
+  MIA_REQUIRE(a->rows == 0 || a->head_dim == 0 || a->src, MIA_ERR_VALUE, "stage: null src");
+  MIA_REQUIRE(a->prior_rows == 0 || a->head_dim == 0 || a->prior, MIA_ERR_VALUE,
+              "stage: null prior");
+  return mia::launch_stage_rows(*a, (hipStream_t)stream);
 }
 
 static void slot_mapping_one(const mia_slot_mapping_args *a, int64_t t) {

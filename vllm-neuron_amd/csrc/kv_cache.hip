@@ -6,6 +6,8 @@
 //   * slot_mapping  : slot = bt[req, pos // bs] * bs + pos % bs (+ DCP variant)
 //   * remap_null    : block-table 0 -> -1
 //   * swa_trim      : sliding-window decode table trim + position offset
+//   * stage_rows    : dense attention K/V/Q staging (prior rows + new rows,
+//                     zero tail and head-dim padding, layout transpose)
 // All are HBM-bound element kernels; each thread owns whole 16-byte chunks
 // where the layout allows it.
 #include "mia_device.h"
@@ -190,6 +192,141 @@ __global__ void scatter_rows_kernel(mia_scatter_rows_args a) {
   }
 }
 
+// A 64-row tile of dst [t0, t0 + 64) x [0, out_dim) of head blockIdx.y goes
+// through LDS so that both sides are coalesced.  The tile is read in units
+// of 8 elements along the source's unit-stride axis (d for row-major
+// sources, the row for d-major ones), one 16-byte load per unit where the
+// unit lies in one region (prior or new rows) whose layout allows it, 8
+// element loads otherwise; rows are then stored as whole 16-byte chunks.
+// The LDS row pitch of 65 words keeps the column writes of d-major tiles
+// free of bank conflicts.
+constexpr int kStageRows = 64;
+constexpr int kStagePitch = 130;  // u16 per LDS row
+
+struct StageRegion {
+  const uint16_t *p;
+  int64_t s0, s1, s2;  // head, row, d strides (elements)
+  bool vec;            // 16-byte unit loads allowed
+};
+
+MIA_DEV uint16_t stage_elem(const StageRegion &g, int64_t h, int64_t t, int64_t e) {
+  return g.p[h * g.s0 + t * g.s1 + e * g.s2];
+}
+
+__global__ __launch_bounds__(256) void stage_rows_kernel(mia_stage_args a) {
+  __shared__ uint16_t tile[kStageRows * kStagePitch];
+  const int64_t h = blockIdx.y;
+  const int t0 = blockIdx.x * kStageRows;
+  const int D = a.head_dim, Dp = a.out_dim, P = a.prior_rows, S = a.rows;
+  const bool row_fast = a.src_stride[1] == 1 && a.src_stride[2] != 1;  // d-major source
+  auto region = [&](const void *p, const int64_t *st, bool vec_extra) {
+    StageRegion g;
+    g.p = (const uint16_t *)p;
+    g.s0 = st[0];
+    g.s1 = st[1];
+    g.s2 = st[2];
+    g.vec = p && ((uintptr_t)p % 16 == 0) && st[0] % 8 == 0 && vec_extra &&
+            (row_fast ? (st[1] == 1 && st[2] % 8 == 0) : (st[2] == 1 && st[1] % 8 == 0));
+    return g;
+  };
+  // d-major units of the new rows start at t - P: 16-byte aligned iff P % 8 == 0
+  const StageRegion src = region(a.src, a.src_stride, row_fast ? P % 8 == 0 : D % 8 == 0);
+  const StageRegion pri = region(a.prior, a.prior_stride, row_fast || D % 8 == 0);
+  const int upr = Dp / 8;  // units per row (row-major walk)
+  constexpr int kUnits = kStageRows * 128 / 8 / 256;  // units per thread at most
+  // A tile takes the vector path when every unit in it is a 16-byte load or
+  // all zeros: its regions allow 16-byte loads and no unit straddles a
+  // region boundary (d-major units are 8 rows, row-major ones 8 d values).
+  const bool has_pri = t0 < P, has_src = S > 0 && t0 < P + S && t0 + kStageRows > P;
+  bool fast = (!has_pri || pri.vec) && (!has_src || src.vec);
+  if (row_fast)
+    fast = fast && P % 8 == 0 &&
+           ((P + S) % 8 == 0 || t0 + kStageRows <= P + S || t0 >= P + S);
+  else
+    fast = fast && D % 8 == 0;
+  u32x4_t w[kUnits];
+  auto unit = [&](int k, int &r, int &e) {  // first element of unit k of the thread
+    const int u = threadIdx.x + k * 256;
+    r = row_fast ? (u & 7) * 8 : u / upr;
+    e = row_fast ? (u >> 3) : (u - (u / upr) * upr) * 8;
+    return u < kStageRows * upr && e < D && t0 + r < P + S;
+  };
+  // all loads of the thread first, then the LDS writes
+  if (fast) {
+    // branch-free: dead units load a valid address of the tile's regions and
+    // are zeroed afterwards, so the loads of a thread issue back to back
+    const bool any = D > 0 && (has_pri || has_src);
+    const uint16_t *safe = has_src ? src.p + h * src.s0 : pri.p + h * pri.s0;
+#pragma unroll
+    for (int k = 0; k < kUnits; ++k) {
+      int r, e;
+      const bool live = unit(k, r, e);
+      const int t = t0 + r;
+      const bool inp = t < P;
+      const uint16_t *base = inp ? pri.p : src.p;
+      const int64_t tt = inp ? t : t - P;
+      const int64_t off = inp ? (h * pri.s0 + (row_fast ? tt + e * pri.s2 : tt * pri.s1 + e))
+                              : (h * src.s0 + (row_fast ? tt + e * src.s2 : tt * src.s1 + e));
+      w[k] = u32x4_t{0u, 0u, 0u, 0u};
+      if (any) {
+        const u32x4_t x = *reinterpret_cast<const u32x4_t *>(live ? base + off : safe);
+        w[k] = live ? x : w[k];
+      }
+    }
+  } else {
+#pragma unroll
+    for (int k = 0; k < kUnits; ++k) {
+      int r, e;
+      const bool live = unit(k, r, e);
+      const int t = t0 + r;
+      uint16_t v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int tj = row_fast ? t + j : t;
+        const int ej = row_fast ? e : e + j;
+        v[j] = 0;
+        if (live && ej < D) {
+          if (tj < P)
+            v[j] = stage_elem(pri, h, tj, ej);
+          else if (tj < P + S)
+            v[j] = stage_elem(src, h, tj - P, ej);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w[k][j] = (uint32_t)v[2 * j] | ((uint32_t)v[2 * j + 1] << 16);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < kUnits; ++k) {
+    const int u = threadIdx.x + k * 256;
+    if (u >= kStageRows * upr) continue;
+    if (row_fast) {
+      const int r = (u & 7) * 8, e = u >> 3;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        tile[(r + 2 * j) * kStagePitch + e] = (uint16_t)(w[k][j] & 0xffffu);
+        tile[(r + 2 * j + 1) * kStagePitch + e] = (uint16_t)(w[k][j] >> 16);
+      }
+    } else {
+      const int r = u / upr, e = (u - r * upr) * 8;
+      uint32_t *tw = reinterpret_cast<uint32_t *>(tile + r * kStagePitch + e);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tw[j] = w[k][j];
+    }
+  }
+  __syncthreads();
+  uint16_t *dst = (uint16_t *)a.dst;
+  for (int c = threadIdx.x; c < kStageRows * upr; c += 256) {
+    const int r = c / upr, ch = c - r * upr;
+    const int t = t0 + r;
+    if (t >= a.out_rows) continue;
+    const uint32_t *w = reinterpret_cast<const uint32_t *>(tile + r * kStagePitch + ch * 8);
+    const u32x4_t q = {w[0], w[1], w[2], w[3]};
+    *reinterpret_cast<u32x4_t *>(dst + h * a.dst_stride[0] + (int64_t)t * a.dst_stride[1] +
+                                 ch * 8) = q;
+  }
+}
+
 __global__ void slot_mapping_kernel(mia_slot_mapping_args a) {
   const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (t >= a.num_tokens) return;
@@ -282,6 +419,12 @@ int launch_scatter_rows(const mia_scatter_rows_args &a, hipStream_t s) {
   if (a.num_rows == 0) return MIA_OK;
   hipLaunchKernelGGL(scatter_rows_kernel, dim3((unsigned)a.num_rows), dim3(64), 0, s, a);
   return check_hip(hipGetLastError(), "scatter_rows launch");
+}
+
+int launch_stage_rows(const mia_stage_args &a, hipStream_t s) {
+  const unsigned tiles = (unsigned)((a.out_rows + kStageRows - 1) / kStageRows);
+  hipLaunchKernelGGL(stage_rows_kernel, dim3(tiles, (unsigned)a.num_heads), dim3(256), 0, s, a);
+  return check_hip(hipGetLastError(), "stage_rows launch");
 }
 
 int launch_slot_mapping(const mia_slot_mapping_args &a, hipStream_t s) {

@@ -29,6 +29,7 @@ int launch_remap_null(const int32_t *in, int32_t *out, int64_t n,
 int launch_swa_trim(const mia_swa_trim_args &a, hipStream_t s);
 int launch_packed_k(const mia_packed_k_args &a, hipStream_t s);
 int launch_scatter_rows(const mia_scatter_rows_args &a, hipStream_t s);
+int launch_stage_rows(const mia_stage_args &a, hipStream_t s);
 
 // Paged decode: split-K plan shared by the workspace query and the launch.
 struct DecodePlan {

@@ -958,7 +958,16 @@ PrefillPlan plan_prefill(const mia_prefill_args &a) {
   const int slots = device_cus() * (pl.dma ? 1 : 2);
   pl.slots = slots;
   int64_t ks = a.split_tokens;
-  if (ks <= 0) {
+  if (ks <= 0 && (a.non_causal || a.bound_min)) {
+    // Every row tile reads the whole key range (equal work per tile): split
+    // only as far as the split grid still runs in one wave of slots (more
+    // chunks add merge traffic without shortening the critical path), and
+    // only into chunks of at least 1024 keys, below which the merge costs
+    // more than the better fill gains.
+    const int64_t n = std::min<int64_t>(8, (int64_t)slots / std::max<int64_t>(1, base_wgs));
+    ks = (n >= 2 && s_ctx >= 2048) ? std::max<int64_t>(1024, (s_ctx + n - 1) / n)
+                                   : (int64_t)1 << 30;
+  } else if (ks <= 0) {
     // Without the sequence lengths on the host, split only long tables
     // (>= 3072 keys) when the row tiles alone do not fill the device twice:
     // chunks of a third of the table (rounded up to 512 keys), at least

@@ -647,3 +647,31 @@ def scatter_rows(rows: torch.Tensor, cache: torch.Tensor, block_idx: torch.Tenso
     a.cache = cache.data_ptr()
     a.cache_stride = _arr(ctypes.c_int64, cs)
     N.check(N.lib().mia_scatter_rows(ctypes.byref(a), N.stream_ptr(dev)), "scatter_rows")
+
+
+def stage_rows(rows: torch.Tensor, prior: Optional[torch.Tensor], prior_rows: int,
+               out_rows: int, out_dim: int) -> torch.Tensor:
+    """``[H, out_rows, out_dim]`` bf16: the first ``prior_rows`` rows of
+    ``prior`` then ``rows`` (both ``[H, *, D]`` views with any strides),
+    zeros in the tail rows and the padded head dims (the prefix
+    concatenation and layout transposes of the dense attention inputs)."""
+    dev = N.require_gpu(rows) if prior is None else N.require_gpu(rows, prior)
+    if rows.dtype != torch.bfloat16 or (prior is not None and prior.dtype != torch.bfloat16):
+        raise NotImplementedError("stage_rows: bf16 only")
+    H, S, D = rows.shape
+    if prior_rows and (prior is None or prior.shape[0] != H or prior.shape[1] < prior_rows
+                       or prior.shape[2] != D):
+        raise ValueError("prior must be [H, >= prior_rows, D]")
+    out = torch.empty((H, out_rows, out_dim), dtype=torch.bfloat16, device=dev)
+    a = N.StageArgs()
+    a.src = rows.data_ptr()
+    a.src_stride = _arr(ctypes.c_int64, list(rows.stride()))
+    if prior_rows:
+        a.prior = prior.data_ptr()
+        a.prior_stride = _arr(ctypes.c_int64, list(prior.stride()))
+    a.dst = out.data_ptr()
+    a.dst_stride = _arr(ctypes.c_int64, [out.stride(0), out.stride(1)])
+    a.num_heads, a.rows, a.prior_rows = H, S, int(prior_rows)
+    a.out_rows, a.head_dim, a.out_dim = int(out_rows), D, int(out_dim)
+    N.check(N.lib().mia_stage_rows(ctypes.byref(a), N.stream_ptr(dev)), "stage_rows")
+    return out

@@ -157,9 +157,17 @@ class ScatterRowsArgs(ctypes.Structure):
     ]
 
 
+class StageArgs(ctypes.Structure):
+    _fields_ = [
+        ("src", c_vp), ("src_stride", c_i64 * 3), ("prior", c_vp), ("prior_stride", c_i64 * 3),
+        ("dst", c_vp), ("dst_stride", c_i64 * 2), ("num_heads", c_i32), ("rows", c_i32),
+        ("prior_rows", c_i32), ("out_rows", c_i32), ("head_dim", c_i32), ("out_dim", c_i32),
+    ]
+
+
 ARGS_STRUCTS = {
     0: KvWriteArgs, 1: GatherArgs, 2: MaskArgs, 3: DecodeArgs, 4: PrefillArgs,
-    5: SlotMappingArgs, 6: PackedKArgs, 7: SwaTrimArgs, 8: ScatterRowsArgs,
+    5: SlotMappingArgs, 6: PackedKArgs, 7: SwaTrimArgs, 8: ScatterRowsArgs, 9: StageArgs,
 }
 
 # Exported symbols (must match include/mia_attn.h).
@@ -168,7 +176,7 @@ EXPORTS = [
     "mia_gather_kv", "mia_decode_mask", "mia_decode_workspace_bytes",
     "mia_paged_decode", "mia_prefill_workspace_bytes", "mia_paged_prefill", "mia_slot_mapping",
     "mia_slot_mapping_host", "mia_remap_null_block", "mia_swa_trim",
-    "mia_packed_k_convert", "mia_scatter_rows",
+    "mia_packed_k_convert", "mia_scatter_rows", "mia_stage_rows",
 ]
 
 _lib = None
@@ -185,7 +193,7 @@ def _declare(lib: ctypes.CDLL) -> None:
                      ("mia_decode_mask", MaskArgs), ("mia_paged_decode", DecodeArgs),
                      ("mia_paged_prefill", PrefillArgs), ("mia_slot_mapping", SlotMappingArgs),
                      ("mia_swa_trim", SwaTrimArgs), ("mia_packed_k_convert", PackedKArgs),
-                     ("mia_scatter_rows", ScatterRowsArgs)):
+                     ("mia_scatter_rows", ScatterRowsArgs), ("mia_stage_rows", StageArgs)):
         fn = getattr(lib, name)
         fn.argtypes = [P(st), c_vp]
         fn.restype = c_i32

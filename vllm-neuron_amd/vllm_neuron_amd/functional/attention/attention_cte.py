@@ -44,6 +44,42 @@ def _key_rows(x: Tensor, tokens_last: bool) -> Tensor:
     return x.transpose(-2, -1) if tokens_last else x
 
 
+def _kernel_rows_ok(x: Tensor, Dp: int) -> bool:
+    """Can the kernels read ``x [H, S, D]`` in place: d == Dp contiguous,
+    16-byte aligned rows and base."""
+    return (x.shape[-1] == Dp and x.stride(-1) == 1 and x.data_ptr() % 16 == 0
+            and (x.stride(0) * 2) % 16 == 0 and (x.stride(1) * 2) % 16 == 0)
+
+
+def _paged_view(rows: Tensor, prior: Optional[Tensor], P: int, Lp: int, Dp: int) -> Tensor:
+    """Keys or values ``[H, S, D]`` (token-major view) as a paged cache
+    ``[Lp/64, H, 64, Dp]`` read through an identity block table.  Used in
+    place when it already is one (no prior rows, d == Dp, whole tiles,
+    aligned), otherwise staged once."""
+    H, S, D = rows.shape
+    if P or S != Lp or not _kernel_rows_ok(rows, Dp):
+        rows = K.stage_rows(rows, prior, P, Lp, Dp)
+    st, sh = rows.stride(1), rows.stride(0)
+    return torch.as_strided(rows, (Lp // _TILE, H, _TILE, Dp), (_TILE * st, sh, st, 1))
+
+
+_META: dict = {}
+
+
+def _metadata(dev, S_q: int, P: int, L: int, nblk: int):
+    """Device copies of cu_seqlens [0, S_q], prior [P], kv_len [L] and the
+    identity block table, made once per shape (read-only)."""
+    key = (str(dev), S_q, P, L, nblk)
+    m = _META.get(key)
+    if m is None:
+        d = torch.tensor([0, S_q, P, L], dtype=torch.int32).to(dev)
+        m = (d[0:2], d[2:3], d[3:4], torch.arange(nblk, dtype=torch.int32, device=dev).view(1, nblk))
+        if len(_META) >= 64:
+            _META.clear()
+        _META[key] = m
+    return m
+
+
 def flash_attention(
     q: Tensor,
     k: Tensor,
@@ -101,34 +137,17 @@ def flash_attention(
     Dp = 64 if D <= 64 else 128
     L = P + S_k
     Lp = max(_TILE, (L + _TILE - 1) // _TILE * _TILE)
-
-    # keys and values, prior rows first, token-major, whole tiles, padded d
-    kb = torch.zeros((B_kv, Lp, Dp), dtype=torch.bfloat16, device=dev)
-    vb = torch.zeros((B_kv, Lp, Dp), dtype=torch.bfloat16, device=dev)
-    if P:
-        kb[:, :P, :D] = _key_rows(k_prior, not tp_k)[:, :P]
-        vb[:, :P, :D] = v_prior[:, :P]
-    kb[:, P:L, :D] = kr
-    vb[:, P:L, :D] = v
     nblk = Lp // _TILE
-    # paged view [blocks, kv heads, 64, Dp] of the buffer, identity table
-    k_cache = torch.as_strided(kb, (nblk, B_kv, _TILE, Dp), (_TILE * Dp, Lp * Dp, Dp, 1))
-    v_cache = torch.as_strided(vb, (nblk, B_kv, _TILE, Dp), (_TILE * Dp, Lp * Dp, Dp, 1))
-    table = torch.arange(nblk, dtype=torch.int32, device=dev).view(1, nblk)
+    k_cache = _paged_view(kr, _key_rows(k_prior, not tp_k) if P else None, P, Lp, Dp)
+    v_cache = _paged_view(v, v_prior if P else None, P, Lp, Dp)
+    cu, prior, kv_len, table = _metadata(dev, S_q, P, L, nblk)
 
     # queries [T = S_q, Hq = B, Dp] and the output through strided views
-    if Dp != D or qr.stride(-1) != 1:
-        qp = torch.zeros((B, S_q, Dp), dtype=torch.bfloat16, device=dev)
-        qp[:, :, :D] = qr
-    else:
-        qp = qr
+    qp = qr if _kernel_rows_ok(qr, Dp) else K.stage_rows(qr, None, 0, S_q, Dp)
     out = torch.empty((B, S_q, Dp), dtype=torch.bfloat16, device=dev)
     q_view = qp.permute(1, 0, 2)
     out_view = out.permute(1, 0, 2)
 
-    cu = torch.tensor([0, S_q], dtype=torch.int32, device=dev)
-    prior = torch.tensor([P], dtype=torch.int32, device=dev)
-    kv_len = torch.tensor([L], dtype=torch.int32, device=dev)
     q_off = int(cp_offset.reshape(-1)[0].item()) if cp_offset is not None else 0
     bmin = bmax = None
     if bound_min is not None:
