@@ -238,7 +238,8 @@ typedef struct {
   int64_t out_stride[4]; /* b, s, hq, d */
   void *workspace;
   size_t workspace_bytes;
-  int32_t split_tokens; /* tokens per split-K chunk; 0 = default */
+  int32_t split_tokens; /* least tokens per streaming wave's share (rounded up to 32);
+                           0 = chosen from the shapes */
   int32_t _pad1;
   /* Optional timing instrumentation: hipEvent_t handles recorded on the
    * stream right before the first and right after the last split-K launch

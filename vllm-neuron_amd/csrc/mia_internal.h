@@ -33,8 +33,9 @@ int launch_stage_rows(const mia_stage_args &a, hipStream_t s);
 
 // Paged decode: split-K plan shared by the workspace query and the launch.
 struct DecodePlan {
-  int split_tokens;  // tokens per split-K chunk
-  int num_splits;    // ceil(S_ctx / split_tokens)
+  int split_tokens;  // min_tiles * 32
+  int min_tiles;     // shortest tile range of a streaming wave
+  int num_splits;    // partial slots per (row, kv head)
   int ncols;         // columns (query token x head of a GQA group) per launch
   int col_groups;    // launches over column groups
   int grid;          // workgroups of the persistent split-K kernel

@@ -2,16 +2,17 @@
 // gfx950 (wave64, MFMA, 160 KB LDS).
 //
 // Work decomposition (split kernel)
-//   The prior context of batch row b, kv head h is cut into chunks of
-//   `split_tokens` tokens; a work item is one (b, h, chunk) that overlaps
-//   the row's attended range.  The grid is persistent (2 or 3 workgroups
-//   of 4 waves per CU); each wave streams items blockIdx*4+wave,
-//   +gridDim*4, ... independently of the other waves.  An item covers every
-//   query column of its GQA group (column = query token s x head g, up to
-//   16 per launch), so each K/V byte is read from HBM once.
-//   Every workgroup first computes each row's attended range and the prefix
-//   sum of items in LDS (rows <= 1024); a wave maps its item id to
-//   (b, h, chunk) by binary search.
+//   The attended prior tiles (32 tokens) of every (batch row b, kv head h)
+//   segment are laid end to end; the grid is persistent (2 or 3 workgroups
+//   of 4 waves per CU) and streaming wave w takes an equal contiguous share
+//   of the tiles, keeping one online-softmax state per segment piece, so
+//   each wave writes one or two partials instead of one per fixed-size
+//   chunk (partial stores delay every later load of the wave).  A piece
+//   covers every query column of its GQA group (column = query token s x
+//   head g, up to 16 per launch), so each K/V byte is read from HBM once.
+//   Every workgroup first computes each row's attended range and the tile
+//   prefix sum in LDS (rows <= 1024); a wave maps a tile to its segment by
+//   binary search.
 //
 // Per 32-token tile and wave
 //   K  : 2 sub-tiles of 16 tokens loaded straight into MFMA A-operand
@@ -56,8 +57,7 @@ constexpr int kWaves = 4;
 constexpr int wg_per_cu(int D, bool fp8) { return (void)D, fp8 ? 3 : 2; }
 constexpr int kTile = 32;  // tokens per wave tile
 constexpr int kPMax = 128;
-constexpr int kMaxSplitTokens = 1024;  // largest chunk (block ids of a chunk fit a wave)
-constexpr int kDefaultChunk = 256;     // tokens per work item
+constexpr int kMaxMinTiles = 8;        // longest minimum tile range of a streaming wave
 constexpr int kMaxRows = 1024;         // batch rows of the persistent decode
 
 // Compute units of the current device (queried once per device).
@@ -95,13 +95,14 @@ struct DecodeKParams {
   int mask_bl;
   float scale_log2;  // softmax_scale * log2(e) (* 256 for the fp8 decode)
   const float *k_deq;
-  int split_tokens;
-  int num_splits;
+  int min_tiles;   // shortest tile range of a streaming wave
+  int num_splits;  // partial slots per (row, kv head): pieces of its tiles
   int nblk;  // block-table width
   int col0;    // first column of this launch
   int nc_tot;  // G * S
   float *ws_o;   // [B, Hkv, num_splits, nc_tot, D]
   float *ws_ml;  // [B, Hkv, num_splits, nc_tot, 2]
+  int *ws_hdr;   // [B + 2]: tile prefix R[0..B], streaming waves W
 };
 
 struct RowInfo {
@@ -190,13 +191,28 @@ struct KLoad<true> {
 // ---------------------------------------------------------------------------
 // split kernel
 // ---------------------------------------------------------------------------
-// One work item of a streaming wave: kv head h of batch row b, chunk c
-// (tokens [c*CH, (c+1)*CH) of the prior range).  All fields are wave
-// uniform.
+// Work decomposition.  The attended prior range [lo, hi) of row b covers
+// T_b = ceil(hi / 32) - floor(lo / 32) tiles of 32 tokens; the tiles of
+// all (row, kv head) segments are laid end to end (row-major, kv heads in
+// order): segment (b, h) is [R[b] + h T_b, R[b] + (h + 1) T_b) with
+// R[b] = sum over rows r < b of Hkv T_r, N = R[B] tiles in total.  Streaming
+// wave w of W takes the contiguous tiles [floor(w N / W), floor((w+1) N / W))
+// — the same number of tiles for every wave, whatever the context lengths —
+// and keeps one online-softmax state across the tiles of a segment, so it
+// writes one partial per segment piece it touches: usually one or two per
+// wave.  The piece of segment (b, h) streamed by wave w goes to slot
+// w - w_first(b, h), where w_first is the wave holding the segment's first
+// tile; the combine kernel enumerates the same slots from R and W.
 struct Item {
-  int valid, b, h, c, t_lo, t_hi, cb0;
+  int valid, b, h, j, t_lo, t_hi;
+  int next_x;  // first tile of the following piece of this wave
   float minpos;
 };
+
+// Wave holding flattened tile x when N tiles are spread over W waves.
+MIA_DEV int wave_of_tile(int64_t x, int n_tiles, int waves) {
+  return (int)(((x + 1) * waves - 1) / n_tiles);
+}
 
 MIA_DEV int wave_scan_incl(int x, int lane) {
 #pragma unroll
@@ -222,17 +238,16 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
   // swizzled by row (chunk c of token row t at c ^ (t % (D/8))): the writes
   // (16 lanes per row) and the transposed reads below are conflict-free
   __shared__ __attribute__((aligned(16))) uint8_t v_lds[kWaves][kTile * D * 2];
-  __shared__ int s_item0[kMaxRows + 1];
+  __shared__ int s_R[kMaxRows + 1];
   __shared__ int s_lo[kMaxRows];
   __shared__ int s_hi[kMaxRows];
   __shared__ float s_minpos[kMaxRows];
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int CH = p.split_tokens;
 
   // ---- setup (every workgroup): prior range of each row and the prefix
-  // sum of work items (rows x kv heads x chunks overlapping the range)
+  // sum R of its tiles over the kv heads
   for (int r = threadIdx.x; r < p.B; r += blockDim.x) {
     const RowInfo ri = row_info(p.pos, p.start, p.mask_mode, p.S, p.s_ctx, r);
     s_lo[r] = ri.lo;
@@ -242,21 +257,29 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
   __syncthreads();
   if (wave == 0) {
     int carry = 0;
-    if (lane == 0) s_item0[0] = 0;
+    if (lane == 0) s_R[0] = 0;
     for (int r0 = 0; r0 < p.B; r0 += 64) {
       const int r = r0 + lane;
       int n = 0;
-      if (r < p.B && s_lo[r] < s_hi[r]) n = ((s_hi[r] - 1) / CH - s_lo[r] / CH + 1) * p.Hkv;
+      if (r < p.B && s_lo[r] < s_hi[r])
+        n = ((s_hi[r] + kTile - 1) / kTile - s_lo[r] / kTile) * p.Hkv;
       const int incl = wave_scan_incl(n, lane) + carry;
-      if (r < p.B) s_item0[r + 1] = incl;
+      if (r < p.B) s_R[r + 1] = incl;
       carry = __shfl(incl, 63, 64);
     }
   }
   __syncthreads();
-  const int n_items = s_item0[p.B];
-  const int n_workers = gridDim.x * kWaves;
-  int item_id = readfirstlane(blockIdx.x * kWaves + wave);
-  if (item_id >= n_items) return;  // no barrier below this point
+  const int n_tiles = s_R[p.B];
+  // streaming waves: all of the grid, or fewer so that each takes at least
+  // min_tiles tiles
+  const int n_waves = max(1, min((int)gridDim.x * kWaves, n_tiles / p.min_tiles));
+  if (blockIdx.x == 0) {  // the combine kernel re-derives the slots from these
+    for (int r = threadIdx.x; r <= p.B; r += blockDim.x) p.ws_hdr[r] = s_R[r];
+    if (threadIdx.x == 0) p.ws_hdr[p.B + 1] = n_waves;
+  }
+  const int w_id = readfirstlane(blockIdx.x * kWaves + wave);
+  if (n_tiles == 0 || w_id >= n_waves) return;  // no barrier below this point
+  const int x_end = (int)((int64_t)(w_id + 1) * n_tiles / n_waves);
 
   // ---- lane roles
   const int qcol = lane & 15;
@@ -269,7 +292,6 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
   const int tl = lane / DS;
   const int k_lane_off = (qcol * (int)p.kc_t + kg * 8) * EB;
   const int v_lane_off = (tl * (int)p.vc_t + ds * 8) * EB;
-  const int max_blk = CH / 16 + 1;  // block ids a chunk can touch (<= 64)
 
   // ---- PV on MFMA: O^T[d, col] += V^T[d, tok] P^T[tok, col] with
   // v_mfma_f32_16x16x32_bf16 per 16-d block.  The contraction index k of
@@ -302,117 +324,174 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
     return (uint32_t)(t * VROWB + ((ds ^ (t & (VNCH - 1))) << 4));
   };
 
-  // Item id -> (b, h, c) by binary search over the prefix sum; an id past
-  // the end yields `fallback` with valid = 0 (so its loads stay in bounds).
-  auto decode_item = [&](int id, const Item &fallback) {
+  // The piece of this wave starting at flattened tile x (x < x_end): its
+  // segment (b, h) by binary search over R, its tokens and partial slot.  An
+  // x past the wave's range yields `fallback` with valid = 0 (so its loads
+  // stay in bounds).
+  auto decode_piece = [&](int x, const Item &fallback) {
     Item it;
-    if (id >= n_items) {
+    if (x >= x_end) {
       it = fallback;
       it.valid = 0;
       return it;
     }
-    int lo = 0, hi = p.B;
+    int lo = 0, hi = p.B;  // s_R[lo] <= x < s_R[hi]
     while (hi - lo > 1) {
       const int mid = (lo + hi) >> 1;
-      if (s_item0[mid] <= id) lo = mid; else hi = mid;
+      if (s_R[mid] <= x) lo = mid; else hi = mid;
     }
     const int b = readfirstlane(lo);
-    const int r = id - readfirstlane(s_item0[b]);
-    const int n_b = (readfirstlane(s_item0[b + 1]) - readfirstlane(s_item0[b])) / p.Hkv;
+    const int r0 = readfirstlane(s_R[b]);
+    const int tb = (readfirstlane(s_R[b + 1]) - r0) / p.Hkv;  // tiles per kv head
     const int row_lo = readfirstlane(s_lo[b]);
     const int row_hi = readfirstlane(s_hi[b]);
+    const int h = (x - r0) / tb;
+    const int seg0 = r0 + h * tb;              // segment start
+    const int end = min(seg0 + tb, x_end);     // piece end
+    const int tile0 = row_lo / kTile + (x - seg0);
     it.valid = 1;
     it.b = b;
-    it.h = r / n_b;
-    it.c = row_lo / CH + (r - it.h * n_b);
-    it.t_lo = max(row_lo, it.c * CH);
-    it.t_hi = min(row_hi, it.c * CH + CH);
-    it.cb0 = (int)fdiv((uint32_t)(it.c * CH), p.bs_div);
+    it.h = h;
+    it.j = w_id - wave_of_tile(seg0, n_tiles, n_waves);
+    it.t_lo = max(row_lo, tile0 * kTile);
+    it.t_hi = min(row_hi, (tile0 + (end - x)) * kTile);
+    it.next_x = end;
     it.minpos = __builtin_bit_cast(float, readfirstlane(__builtin_bit_cast(int, s_minpos[b])));
     return it;
   };
-  // Per-item vector data: block ids (lane j = block cb0 + j), Q columns,
-  // sliding-window start of this lane's column.
-  auto load_blocks = [&](const Item &it) {
-    const int n = min(max_blk, p.nblk - it.cb0);
-    const int j = min(lane, n - 1);
-    int32_t v = p.bt[(int64_t)it.b * p.bt_b + (int64_t)it.h * p.bt_h +
-                     (int64_t)(it.cb0 + j) * p.bt_j];
-    return v < 0 ? 0 : (v >= p.nb ? p.nb - 1 : v);
-  };
+  // Per-piece vector data, loaded one piece ahead and read by nothing before
+  // that piece (Q columns past the group load column 0 and are masked
+  // through their scores), so the loads never stall the wave at a piece
+  // boundary: Q columns, sliding-window start of this lane's column, K
+  // dequant scale.
   auto load_q = [&](const Item &it, bf16x8_t (&qf)[KSTEPS]) {
     const uint16_t *qp = p.q + it.b * p.qs_b + (int64_t)s_q * p.qs_s +
                          (int64_t)(it.h * p.G + g_q) * p.qs_h;
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) {
-      u32x4_t w = *reinterpret_cast<const u32x4_t *>(qp + ks * 32 + kg * 8);
-      if (!col_ok) w = u32x4_t{0u, 0u, 0u, 0u};
-      qf[ks] = __builtin_bit_cast(bf16x8_t, w);
-    }
+    for (int ks = 0; ks < KSTEPS; ++ks)
+      qf[ks] = __builtin_bit_cast(bf16x8_t,
+                                  *reinterpret_cast<const u32x4_t *>(qp + ks * 32 + kg * 8));
   };
   auto load_start = [&](const Item &it) {
     return (p.mask_mode == 0 && p.start) ? p.start[(int64_t)it.b * p.S + s_q] : 0.f;
   };
-
-  // Loads are unconditional: every address is taken from a wave-uniform,
-  // clamped group start inside [t_lo, t_hi) of the item (so it lies in an
-  // attended, allocated block); rows outside the range are masked
-  // afterwards (scores to -inf, V rows to zero).  A predicated load would
-  // make the compiler wait for each load before writing the zero of the
-  // inactive lanes.
-  auto issue_k = [&](raw_t (&kr)[NSUB][KSTEPS], const Item &it, int blk, int t0) {
+  auto load_kdeq = [&](const Item &it) { return p.k_deq ? p.k_deq[it.h] : 1.0f; };
+  // Physical block of table entry bi of a piece, read with a scalar load
+  // (uniform address; consecutive tiles hit the scalar cache).  Scalar loads
+  // are counted apart from the vector loads, so they never make the wave
+  // wait for its in-flight K/V tiles.  Out-of-range ids are clamped.
+  typedef const __attribute__((address_space(4))) int32_t const_i32_t;
+  const_i32_t *const bt_s = (const_i32_t *)p.bt;
+  auto block_at = [&](const Item &it, int bi) {
+    const int j = min(bi, p.nblk - 1);
+    const int32_t v = bt_s[(int64_t)it.b * p.bt_b + (int64_t)it.h * p.bt_h + (int64_t)j * p.bt_j];
+    return v < 0 ? 0 : (v >= p.nb ? p.nb - 1 : v);
+  };
+  // Blocks of the two 16-token groups of the tile at t0: a group (16
+  // tokens, aligned) lies in one block as block_size % 16 == 0.  Loads are
+  // unconditional: every address is clamped into [t_lo, t_hi) of the piece
+  // (K per group, V per row of TL tokens; a clamped V row stays in its
+  // group's clamped block since TL divides 16), so it lies in an attended,
+  // allocated block, and rows outside the range are masked after the load
+  // (scores to -inf, V rows to zero).  A predicated load would make the
+  // compiler wait for each load before writing the zero of inactive lanes.
+  struct TileRef {
+    int tb[NSUB];  // clamped group start
+    int bi[NSUB];  // its table entry
+    int32_t phys[NSUB];
+  };
+  auto tile_ref = [&](const Item &it, int t0) {
+    TileRef r;
     const int k_first = (it.t_lo >> 4) << 4, k_last = ((it.t_hi - 1) >> 4) << 4;
+#pragma unroll
+    for (int st = 0; st < NSUB; ++st) {
+      r.tb[st] = min(max(t0 + st * 16, k_first), k_last);  // uniform
+      r.bi[st] = (int)fdiv((uint32_t)r.tb[st], p.bs_div);
+      r.phys[st] = block_at(it, r.bi[st]);
+    }
+    return r;
+  };
+  auto issue_k = [&](raw_t (&kr)[NSUB][KSTEPS], const Item &it, const TileRef &r) {
     const uint8_t *kbase = p.k_cache + (int64_t)it.h * p.kc_h * EB;
 #pragma unroll
     for (int st = 0; st < NSUB; ++st) {
-      const int tb = min(max(t0 + st * 16, k_first), k_last);  // uniform
-      const int bi = (int)fdiv((uint32_t)tb, p.bs_div);
-      const int32_t phys = __builtin_amdgcn_readlane(blk, bi - it.cb0);
-      const uint8_t *kp = kbase + ((int64_t)phys * p.kc_blk +
-                                   (int64_t)(tb - bi * p.bs) * p.kc_t) * EB;
+      const uint8_t *kp = kbase + ((int64_t)r.phys[st] * p.kc_blk +
+                                   (int64_t)(r.tb[st] - r.bi[st] * p.bs) * p.kc_t) * EB;
 #pragma unroll
       for (int ks = 0; ks < KSTEPS; ++ks)
         kr[st][ks] = KL::load(kp + k_lane_off + ks * 32 * EB);
     }
   };
-  auto issue_v = [&](raw_t (&vr)[VPL], const Item &it, int blk, int t0) {
+  auto issue_v = [&](raw_t (&vr)[VPL], const Item &it, const TileRef &r, int t0) {
     const int v_first = (it.t_lo / TL) * TL, v_last = ((it.t_hi - 1) / TL) * TL;
     const uint8_t *vbase = p.v_cache + (int64_t)it.h * p.vc_h * EB;
 #pragma unroll
     for (int i = 0; i < VPL; ++i) {
+      const int st = (i * TL) / 16;
       const int tb = min(max(t0 + i * TL, v_first), v_last);  // uniform
-      const int bi = (int)fdiv((uint32_t)tb, p.bs_div);
-      const int32_t phys = __builtin_amdgcn_readlane(blk, bi - it.cb0);
-      const uint8_t *vp = vbase + ((int64_t)phys * p.vc_blk +
-                                   (int64_t)(tb - bi * p.bs) * p.vc_t) * EB;
+      const uint8_t *vp = vbase + ((int64_t)r.phys[st] * p.vc_blk +
+                                   (int64_t)(tb - r.bi[st] * p.bs) * p.vc_t) * EB;
       vr[i] = KL::load(vp + v_lane_off);
     }
   };
   auto first_tile = [&](const Item &it) { return (it.t_lo / kTile) * kTile; };
 
-  // ---- the stream: this wave's items (every n_workers-th), tile after
-  // tile; the next tile's K (V) loads are issued as soon as QK (PV) has
-  // consumed the registers, across item boundaries, so one tile of loads
-  // is always in flight.  Past the last item the prefetch re-reads the
-  // current tile (an L2 hit): no load is conditional.
-  Item cur = decode_item(item_id, Item{});
-  int blk_cur = load_blocks(cur);
+  // ---- the stream: this wave's pieces, tile after tile; the next tile's K
+  // (V) loads are issued as soon as QK (PV) has consumed the registers,
+  // across piece boundaries, so one tile of loads is always in flight.  Past
+  // the last piece the prefetch re-reads the current tile (an L2 hit): no
+  // load is conditional.
+  // Partial of one piece: (o, m, l) of its NCP columns.  The columns are
+  // NCP * D contiguous floats of the workspace; they go through the wave's
+  // V tile in LDS (idle between tiles) so that every global store writes 16
+  // contiguous bytes per lane, whole rows, not 64-byte pieces from a quarter
+  // of the lanes.
+  auto write_partial = [&](const f32x4_t (&o)[DB16], float m, float l, int64_t ws_row, int j) {
+    if (j >= p.num_splits) return;  // never: a segment has at most num_splits pieces
+    typedef __attribute__((address_space(3))) f32x4_t lds_f32x4_t;
+#pragma unroll
+    for (int blk = 0; blk < DB16; ++blk)  // [column][d] in LDS (16 x D floats)
+      *(lds_f32x4_t *)(vw + (qcol * D + 16 * blk + 4 * kg) * 4) = o[blk];
+    const int nvalid = min(NCP, p.nc_tot - p.col0);  // columns with workspace rows
+    float *const dst = p.ws_o + (ws_row + p.col0) * D;
+    constexpr int kStores = NCP * D * 4 / 1024;       // 16 bytes per lane each
+#pragma unroll
+    for (int s = 0; s < kStores; ++s) {
+      const int e = s * 256 + lane * 4;  // float index in the piece's NCP x D block
+      if (e / D < nvalid)
+        *reinterpret_cast<f32x4_t *>(dst + e) = *(lds_f32x4_t *)(vw + e * 4);
+    }
+    if (lane < nvalid)
+      *reinterpret_cast<float2 *>(p.ws_ml + (ws_row + p.col0 + lane) * 2) = make_float2(m, l);
+  };
+  Item cur = decode_piece((int)((int64_t)w_id * n_tiles / n_waves), Item{});
   bf16x8_t q_cur[KSTEPS];
   load_q(cur, q_cur);
   float st_cur = load_start(cur);
+  float kdq_cur = load_kdeq(cur);
+  // Per-piece data of the next piece lands in q_land/st_land/kdq_land at the
+  // start of a piece and is copied to the hold registers right after each
+  // tile's V wait, which the landing loads precede in issue order: the copy
+  // costs no wait of its own, and the landing registers are free again when
+  // the next piece reloads them (no wait on a register still being loaded).
+  bf16x8_t q_hold[KSTEPS];
+  float st_hold = 0.f, kdq_hold = 1.f;
   raw_t kr[NSUB][KSTEPS];
   raw_t vr[VPL];
-  issue_k(kr, cur, blk_cur, first_tile(cur));
-  issue_v(vr, cur, blk_cur, first_tile(cur));
+  {
+    const TileRef r0 = tile_ref(cur, first_tile(cur));
+    issue_k(kr, cur, r0);
+    issue_v(vr, cur, r0, first_tile(cur));
+  }
 
   while (true) {
-    const Item nxt = decode_item(item_id + n_workers, cur);
-    const int blk_nxt = load_blocks(nxt);
-    bf16x8_t q_nxt[KSTEPS];
-    load_q(nxt, q_nxt);
-    const float st_nxt = load_start(nxt);
+    const Item nxt = decode_piece(cur.next_x, cur);
+    bf16x8_t q_land[KSTEPS];
+    load_q(nxt, q_land);
+    const float st_land = load_start(nxt);
+    const float kdq_land = load_kdeq(nxt);
 
-    const float scale2 = p.scale_log2 * (p.k_deq ? p.k_deq[cur.h] : 1.0f);
+    const float scale2 = p.scale_log2 * kdq_cur;
     const bool wrap_q = st_cur > cur.minpos;
     float m_run = -INFINITY;  // per column (lane & 15)
     float l_run = 0.f;        // per lane partial
@@ -427,8 +506,8 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
       const bool last = t0 + kTile >= cur.t_hi;
       const bool to_next = last && nxt.valid;
       const Item &itN = to_next ? nxt : cur;
-      const int blkN = to_next ? blk_nxt : blk_cur;
       const int tN = to_next ? first_tile(nxt) : (last ? t0 : t0 + kTile);
+      const TileRef rN = tile_ref(itN, tN);  // scalar loads, in flight during QK
 
       // ---- QK^T on MFMA
       float sc[NSUB][4];
@@ -442,7 +521,7 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
 #pragma unroll
         for (int i = 0; i < 4; ++i) sc[st][i] = acc[i];
       }
-      issue_k(kr, itN, blkN, tN);
+      issue_k(kr, itN, rN);
 #pragma unroll
       for (int st = 0; st < NSUB; ++st) {
 #pragma unroll
@@ -477,7 +556,13 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
         *(__attribute__((address_space(3))) u32x4_t *)(vw + v_wr_off(i)) =
             __builtin_bit_cast(u32x4_t, KL::to_bf16(rv));
       }
-      issue_v(vr, itN, blkN, tN);
+      issue_v(vr, itN, rN, tN);
+      // (every tile: cheap moves, and then no path leaves the landing loads
+      // pending, so the compiler never waits on them elsewhere)
+#pragma unroll
+      for (int ks = 0; ks < KSTEPS; ++ks) q_hold[ks] = q_land[ks];
+      st_hold = st_land;
+      kdq_hold = kdq_land;
       // ---- online softmax (exp2 domain) with lazy rescaling: the running
       // max only moves when the tile's max exceeds it by more than 8, so the
       // accumulators are rescaled only on such tiles
@@ -526,28 +611,18 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
       }
     }
 
-    // ---- item epilogue: reduce within the wave, write the partial
+    // ---- piece epilogue: reduce within the wave, then write the partial
     l_run = wave_sum_xor(l_run, 16);
     l_run = wave_sum_xor(l_run, 32);
-    const int64_t ws_row = (((int64_t)cur.b * p.Hkv + cur.h) * p.num_splits + cur.c) * p.nc_tot;
-    if (col_ok) {
-      float *dst = p.ws_o + (ws_row + gcol) * D + 4 * kg;
-#pragma unroll
-      for (int blk = 0; blk < DB16; ++blk)
-        *reinterpret_cast<f32x4_t *>(dst + blk * 16) = oacc[blk];
-    }
-    if (lane < NCP && p.col0 + lane < p.nc_tot) {
-      p.ws_ml[(ws_row + p.col0 + lane) * 2] = m_run;
-      p.ws_ml[(ws_row + p.col0 + lane) * 2 + 1] = l_run;
-    }
+    const int64_t ws_row = (((int64_t)cur.b * p.Hkv + cur.h) * p.num_splits + cur.j) * p.nc_tot;
+    write_partial(oacc, m_run, l_run, ws_row, cur.j);
 
     if (!nxt.valid) break;
-    item_id += n_workers;
     cur = nxt;
-    blk_cur = blk_nxt;
 #pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) q_cur[ks] = q_nxt[ks];
-    st_cur = st_nxt;
+    for (int ks = 0; ks < KSTEPS; ++ks) q_cur[ks] = q_hold[ks];
+    st_cur = st_hold;
+    kdq_cur = kdq_hold;
   }
 }
 
@@ -634,8 +709,16 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(CombineParams c) {
 #pragma unroll
   for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
   if (ri.lo < ri.hi) {
-    const int sp0 = ri.lo / p.split_tokens;
-    const int sp1 = (ri.hi + p.split_tokens - 1) / p.split_tokens;
+    // the pieces of segment (b, h): one per streaming wave that held one of
+    // its tiles (tile prefix and wave count written by the split kernel)
+    const int r0 = p.ws_hdr[b], r1 = p.ws_hdr[b + 1];
+    const int n_tiles = p.ws_hdr[p.B], n_waves = p.ws_hdr[p.B + 1];
+    const int tb = (r1 - r0) / p.Hkv;
+    const int seg0 = r0 + h * tb;
+    const int sp0 = 0;
+    const int sp1 = min(wave_of_tile(seg0 + tb - 1, n_tiles, n_waves) -
+                            wave_of_tile(seg0, n_tiles, n_waves) + 1,
+                        p.num_splits);
     const int64_t row0 = ((int64_t)b * p.Hkv + h) * p.num_splits;
     for (int s0 = sp0; s0 < sp1; s0 += kSplitBatch) {
       float ms[kSplitBatch], ls[kSplitBatch], os[kSplitBatch][DPL];
@@ -777,39 +860,37 @@ DecodePlan plan_decode(const mia_decode_args &a) {
   DecodePlan pl;
   const int G = a.num_q_heads / a.num_kv_heads;
   const int s_ctx = a.blocks_per_seq * a.block_size;
-  // Work items are (row, kv head, chunk of split_tokens tokens); each is
-  // streamed by one wave.  The chunk is a shape-only choice (graph
-  // capturable, no host sync), a multiple of the 32-token tile whose block
-  // ids fit in one wave register.
+  // Streaming waves take equal contiguous shares of the attended tiles, at
+  // least min_tiles each (a shape-only choice: graph capturable, no host
+  // sync).  Large problems use every wave of the grid; small ones fewer,
+  // down to single tiles, so that the work still spreads.  A segment of at
+  // most t_max tiles then meets at most ceil(t_max / min_tiles) + 1 waves:
+  // its partial slots.
   const int wgs_cu = wg_per_cu(a.head_dim, a.cache_dtype == MIA_DTYPE_FP8_E4M3FN);
-  int st = a.split_tokens;
-  if (st <= 0) {
-    // about 8 worst-case items per streaming wave, 32..256 tokens each:
-    // small problems get short items so that every wave has work.
-    const int64_t waves = wgs_cu * (int64_t)device_cu_count() * kWaves;
-    const int64_t tokens = (int64_t)a.batch * a.num_kv_heads * s_ctx;
-    const int64_t want = tokens / (8 * waves);
-    st = kTile;
-    while (st < want && st < kDefaultChunk) st <<= 1;
-  }
-  st = ((st + kTile - 1) / kTile) * kTile;
-  const int st_cap = std::min(kMaxSplitTokens, (63 * a.block_size / kTile) * kTile);
-  if (st > st_cap) st = st_cap;
-  pl.split_tokens = st;
-  pl.num_splits = s_ctx > 0 ? (s_ctx + st - 1) / st : 0;
-  if (pl.num_splits < 1) pl.num_splits = 1;
+  const int64_t waves = wgs_cu * (int64_t)device_cu_count() * kWaves;
+  const int t_max = (s_ctx + kTile - 1) / kTile;
+  const int64_t n_max = (int64_t)a.batch * a.num_kv_heads * t_max;
+  int mt;
+  if (a.split_tokens > 0)
+    mt = (a.split_tokens + kTile - 1) / kTile;
+  else
+    mt = (int)std::min<int64_t>(kMaxMinTiles, std::max<int64_t>(1, n_max / (2 * waves)));
+  pl.min_tiles = mt;
+  pl.split_tokens = mt * kTile;
+  pl.num_splits = t_max > 0 ? (t_max + mt - 1) / mt + 1 : 1;
   pl.ncols = G * a.s_active;
   pl.col_groups = (pl.ncols + 15) / 16;
   // persistent grid: wg_per_cu workgroups of four streaming waves per CU,
-  // or fewer when the worst-case item count is smaller
-  const int64_t max_items = (int64_t)a.batch * a.num_kv_heads * pl.num_splits;
-  int64_t wg = (max_items + kWaves - 1) / kWaves;
+  // or fewer when fewer waves can have min_tiles tiles each
+  const int64_t wg = (std::max<int64_t>(1, n_max / mt) + kWaves - 1) / kWaves;
   const int64_t cap = wgs_cu * (int64_t)device_cu_count();
   pl.grid = (int)std::max<int64_t>(1, std::min(wg, cap));
   const size_t rows = (size_t)a.batch * a.num_kv_heads * pl.num_splits * pl.ncols;
   size_t o_bytes = rows * (size_t)a.head_dim * sizeof(float);
   o_bytes = (o_bytes + 255) & ~(size_t)255;
-  pl.ws_bytes = o_bytes + rows * 2 * sizeof(float);
+  size_t ml_bytes = rows * 2 * sizeof(float);
+  ml_bytes = (ml_bytes + 255) & ~(size_t)255;
+  pl.ws_bytes = o_bytes + ml_bytes + ((size_t)a.batch + 2) * sizeof(int32_t);
   return pl;
 }
 
@@ -850,15 +931,18 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
   kp.mask_bl = a.mask_block_len;
   kp.scale_log2 = a.softmax_scale * kLog2e * (fp8 ? 256.0f : 1.0f);
   kp.k_deq = a.k_dequant;
-  kp.split_tokens = pl.split_tokens;
+  kp.min_tiles = pl.min_tiles;
   kp.nblk = a.blocks_per_seq;
   kp.num_splits = pl.num_splits;
   kp.nc_tot = pl.ncols;
   const size_t rows = (size_t)a.batch * a.num_kv_heads * pl.num_splits * pl.ncols;
   size_t o_bytes = rows * (size_t)a.head_dim * sizeof(float);
   o_bytes = (o_bytes + 255) & ~(size_t)255;
+  size_t ml_bytes = rows * 2 * sizeof(float);
+  ml_bytes = (ml_bytes + 255) & ~(size_t)255;
   kp.ws_o = (float *)a.workspace;
   kp.ws_ml = (float *)((char *)a.workspace + o_bytes);
+  kp.ws_hdr = (int *)((char *)a.workspace + o_bytes + ml_bytes);
 
   const dim3 grid((unsigned)pl.grid);
   if (a.split_event_begin) {
