@@ -202,7 +202,9 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=50)
-    ap.add_argument("--warmup", type=int, default=10)
+    # 100 untimed steps (~22 ms): with 10 the timed steps of some runs ran
+    # ~10 % slower (clocks still ramping), with 100 or more they never did
+    ap.add_argument("--warmup", type=int, default=100)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-rows", type=int, default=16,
                     help="batch rows of the decode batch timed on the CPU")

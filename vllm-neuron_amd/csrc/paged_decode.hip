@@ -4,8 +4,9 @@
 // Work decomposition (split kernel)
 //   The attended prior tiles (32 tokens) of every (batch row b, kv head h)
 //   segment are laid end to end; the grid is persistent (2 or 3 workgroups
-//   of 4 waves per CU) and streaming wave w takes an equal contiguous share
-//   of the tiles, keeping one online-softmax state per segment piece, so
+//   of 4 waves per CU) and streaming wave w takes a contiguous share of the
+//   tiles (weighted by dispatch class: earlier workgroups on a CU issue
+//   first and stream faster), keeping one online-softmax state per segment piece, so
 //   each wave writes one or two partials instead of one per fixed-size
 //   chunk (partial stores delay every later load of the wave).  A piece
 //   covers every query column of its GQA group (column = query token s x
@@ -58,6 +59,9 @@ constexpr int wg_per_cu(int D, bool fp8) { return (void)D, fp8 ? 3 : 2; }
 constexpr int kTile = 32;  // tokens per wave tile
 constexpr int kPMax = 128;
 constexpr int kMaxMinTiles = 8;        // longest minimum tile range of a streaming wave
+// share weight of a streaming wave by dispatch class (see share_prefix)
+constexpr int kClassWeightBf16[3] = {5, 4, 4};
+constexpr int kClassWeightFp8[3] = {6, 5, 4};
 constexpr int kMaxRows = 1024;         // batch rows of the persistent decode
 
 // Compute units of the current device (queried once per device).
@@ -96,6 +100,8 @@ struct DecodeKParams {
   float scale_log2;  // softmax_scale * log2(e) (* 256 for the fp8 decode)
   const float *k_deq;
   int min_tiles;   // shortest tile range of a streaming wave
+  int class_waves; // streaming waves per dispatch class (4 x compute units)
+  int cls_w[3];    // share weight of a wave of dispatch class 0, 1, 2
   int num_splits;  // partial slots per (row, kv head): pieces of its tiles
   int nblk;  // block-table width
   int col0;    // first column of this launch
@@ -196,9 +202,10 @@ struct KLoad<true> {
 // all (row, kv head) segments are laid end to end (row-major, kv heads in
 // order): segment (b, h) is [R[b] + h T_b, R[b] + (h + 1) T_b) with
 // R[b] = sum over rows r < b of Hkv T_r, N = R[B] tiles in total.  Streaming
-// wave w of W takes the contiguous tiles [floor(w N / W), floor((w+1) N / W))
-// — the same number of tiles for every wave, whatever the context lengths —
-// and keeps one online-softmax state across the tiles of a segment, so it
+// wave w of W takes the contiguous tiles [share_start(w), share_start(w+1))
+// — shares weighted only by the wave's dispatch class (below), whatever the
+// context lengths — and keeps one online-softmax state across the tiles of
+// a segment, so it
 // writes one partial per segment piece it touches: usually one or two per
 // wave.  The piece of segment (b, h) streamed by wave w goes to slot
 // w - w_first(b, h), where w_first is the wave holding the segment's first
@@ -209,9 +216,41 @@ struct Item {
   float minpos;
 };
 
-// Wave holding flattened tile x when N tiles are spread over W waves.
-MIA_DEV int wave_of_tile(int64_t x, int n_tiles, int waves) {
-  return (int)(((x + 1) * waves - 1) / n_tiles);
+// Shares.  The persistent grid puts wg_per_cu workgroups on every CU,
+// dispatched in order: workgroup g belongs to dispatch class g / CUs, and
+// a SIMD issues the oldest wave first, so waves of earlier classes stream
+// faster (measured on the Llama-3-8B decode with equal shares: first-class
+// waves ended at 151 us on average, second-class ones at 186 us).  Waves
+// therefore take shares weighted by class, cls_w[c] per wave (set by the
+// host per kernel variant; non-increasing).
+
+// Weighted position of the start of wave w's share: sum of the weights of
+// waves [0, w).
+MIA_DEV int64_t share_prefix(const DecodeKParams &p, int w) {
+  int64_t c = 0;
+  int rest = w;
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const int n = (k == 2) ? rest : min(rest, p.class_waves);
+    c += (int64_t)p.cls_w[k] * n;
+    rest -= n;
+  }
+  return c;
+}
+
+// First tile of wave w's share when N tiles are spread over W waves.
+MIA_DEV int64_t share_start(const DecodeKParams &p, int w, int n_tiles, int waves) {
+  return (int64_t)n_tiles * share_prefix(p, w) / share_prefix(p, waves);
+}
+
+// Wave holding flattened tile x: the last w with share_start(w) <= x.
+MIA_DEV int wave_of_tile(const DecodeKParams &p, int64_t x, int n_tiles, int waves) {
+  int lo = 0, hi = waves;  // share_start(lo) <= x < share_start(hi) = N
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (share_start(p, mid, n_tiles, waves) <= x) lo = mid; else hi = mid;
+  }
+  return lo;
 }
 
 MIA_DEV int wave_scan_incl(int x, int lane) {
@@ -270,16 +309,23 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
   }
   __syncthreads();
   const int n_tiles = s_R[p.B];
-  // streaming waves: all of the grid, or fewer so that each takes at least
-  // min_tiles tiles
-  const int n_waves = max(1, min((int)gridDim.x * kWaves, n_tiles / p.min_tiles));
+  // streaming waves: all of the grid, or fewer so that every share holds at
+  // least min_tiles tiles after rounding (the lightest share is
+  // cls_w[2] / cls_w[0] of the heaviest, and shares are rounded down by
+  // less than one tile)
+  const int n_waves =
+      max(1, min((int)gridDim.x * kWaves,
+                 (int)((int64_t)n_tiles * p.cls_w[2] /
+                       ((int64_t)p.cls_w[0] * (p.min_tiles + 1)))));
   if (blockIdx.x == 0) {  // the combine kernel re-derives the slots from these
     for (int r = threadIdx.x; r <= p.B; r += blockDim.x) p.ws_hdr[r] = s_R[r];
     if (threadIdx.x == 0) p.ws_hdr[p.B + 1] = n_waves;
   }
   const int w_id = readfirstlane(blockIdx.x * kWaves + wave);
   if (n_tiles == 0 || w_id >= n_waves) return;  // no barrier below this point
-  const int x_end = (int)((int64_t)(w_id + 1) * n_tiles / n_waves);
+  const int x_begin = (int)share_start(p, w_id, n_tiles, n_waves);
+  const int x_end = (int)share_start(p, w_id + 1, n_tiles, n_waves);
+  if (x_begin >= x_end) return;
 
   // ---- lane roles
   const int qcol = lane & 15;
@@ -352,7 +398,7 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
     it.valid = 1;
     it.b = b;
     it.h = h;
-    it.j = w_id - wave_of_tile(seg0, n_tiles, n_waves);
+    it.j = w_id - wave_of_tile(p, seg0, n_tiles, n_waves);
     it.t_lo = max(row_lo, tile0 * kTile);
     it.t_hi = min(row_hi, (tile0 + (end - x)) * kTile);
     it.next_x = end;
@@ -464,7 +510,7 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
     if (lane < nvalid)
       *reinterpret_cast<float2 *>(p.ws_ml + (ws_row + p.col0 + lane) * 2) = make_float2(m, l);
   };
-  Item cur = decode_piece((int)((int64_t)w_id * n_tiles / n_waves), Item{});
+  Item cur = decode_piece(x_begin, Item{});
   bf16x8_t q_cur[KSTEPS];
   load_q(cur, q_cur);
   float st_cur = load_start(cur);
@@ -655,7 +701,7 @@ struct CombineParams {
 };
 
 constexpr int kMaxAct = 16;
-constexpr int kSplitBatch = 16;
+constexpr int kSplitBatch = 8;
 
 MIA_DEV float quant_roundtrip(const CombineParams &c, float x, int h, const float *qscale) {
   if (c.quant_mode == MIA_QUANT_NONE) return x;
@@ -716,8 +762,8 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(CombineParams c) {
     const int tb = (r1 - r0) / p.Hkv;
     const int seg0 = r0 + h * tb;
     const int sp0 = 0;
-    const int sp1 = min(wave_of_tile(seg0 + tb - 1, n_tiles, n_waves) -
-                            wave_of_tile(seg0, n_tiles, n_waves) + 1,
+    const int sp1 = min(wave_of_tile(p, seg0 + tb - 1, n_tiles, n_waves) -
+                            wave_of_tile(p, seg0, n_tiles, n_waves) + 1,
                         p.num_splits);
     const int64_t row0 = ((int64_t)b * p.Hkv + h) * p.num_splits;
     for (int s0 = sp0; s0 < sp1; s0 += kSplitBatch) {
@@ -860,8 +906,8 @@ DecodePlan plan_decode(const mia_decode_args &a) {
   DecodePlan pl;
   const int G = a.num_q_heads / a.num_kv_heads;
   const int s_ctx = a.blocks_per_seq * a.block_size;
-  // Streaming waves take equal contiguous shares of the attended tiles, at
-  // least min_tiles each (a shape-only choice: graph capturable, no host
+  // Streaming waves take contiguous, class-weighted shares of the attended
+  // tiles, at least min_tiles each (a shape-only choice: graph capturable, no host
   // sync).  Large problems use every wave of the grid; small ones fewer,
   // down to single tiles, so that the work still spreads.  A segment of at
   // most t_max tiles then meets at most ceil(t_max / min_tiles) + 1 waves:
@@ -932,6 +978,11 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
   kp.scale_log2 = a.softmax_scale * kLog2e * (fp8 ? 256.0f : 1.0f);
   kp.k_deq = a.k_dequant;
   kp.min_tiles = pl.min_tiles;
+  kp.class_waves = device_cu_count() * kWaves;
+  // share weights by dispatch class (measured: bf16, two workgroups per CU;
+  // FP8, three)
+  const int *cw = fp8 ? kClassWeightFp8 : kClassWeightBf16;
+  for (int k = 0; k < 3; ++k) kp.cls_w[k] = cw[k];
   kp.nblk = a.blocks_per_seq;
   kp.num_splits = pl.num_splits;
   kp.nc_tot = pl.ncols;

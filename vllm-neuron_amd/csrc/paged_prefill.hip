@@ -878,11 +878,17 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillKParams p) 
         p.ws + (((int64_t)seq * p.Hkv + h) * p.rows_max + r) * p.nsplit * (int64_t)(D + 2);
 #pragma unroll
     for (int j = 0; j < kMaxSp; ++j) {
-      const float *w = w0 + min(j, n_sp - 1) * (D + 2);
-      m[i][j] = w[D];
-      l[i][j] = w[D + 1];
+      m[i][j] = -INFINITY;
+      l[i][j] = 0.f;
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) o[i][j][e] = w[lane * DPL + e];
+      for (int e = 0; e < DPL; ++e) o[i][j][e] = 0.f;
+      if (j < n_sp) {  // only the chunks that exist (uniform)
+        const float *w = w0 + j * (D + 2);
+        m[i][j] = w[D];
+        l[i][j] = w[D + 1];
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) o[i][j][e] = w[lane * DPL + e];
+      }
     }
   }
 #pragma unroll
