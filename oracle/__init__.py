@@ -14,6 +14,7 @@ Modules
   mask       gen_attention_decode_mask torch path and its index helpers
   segmented  _torch_segmented_attention_impl (+ fp32 textbook math)
   dense      _torch_attention_impl of flash_attention (+ float64 textbook)
+  swa_fused  _torch_swa_fused_impl of the fused SWA layer (+ RoPE rotation)
   slots      slot mapping, null-block remap, SWA trim (numpy)
   fp8        FP8 e4m3fn quantisation conventions
   packed     packed FP8 K swizzle / unswizzle / scatter_packed_k

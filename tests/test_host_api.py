@@ -67,6 +67,26 @@ def test_flash_attention_argument_contract():
                         torch.zeros(2, 16, 160, dtype=torch.bfloat16))
 
 
+def test_swa_fused_refuses_cpu_tensors():
+    from vllm_neuron_amd.functional import swa_fused_attention
+    B, S, H, Hq, Hkv, d, bs = 1, 128, 64, 4, 2, 32, 64
+    nq = (Hq + 2 * Hkv) * d
+    kc = torch.zeros(6, Hkv, bs, d, dtype=torch.bfloat16)
+    args = dict(hidden_states=torch.zeros(B, S, H, dtype=torch.bfloat16),
+                qkv_weight=torch.zeros(H, nq, dtype=torch.bfloat16),
+                op_weight=torch.zeros(Hq * d, H, dtype=torch.bfloat16), k_cache=kc,
+                v_cache=kc.clone(), block_tables=torch.ones(B, 4, dtype=torch.int32),
+                cos_cache=torch.ones(B, S, d), sin_cache=torch.zeros(B, S, d),
+                sink=torch.zeros(B, Hq), prior_tokens=torch.zeros(1, 1, dtype=torch.int32),
+                qkv_bias=torch.zeros(1, nq, dtype=torch.bfloat16),
+                op_bias=torch.zeros(1, H, dtype=torch.bfloat16), scale=0.1, sliding_window=64,
+                block_size=bs, num_q_heads=Hq, num_kv_heads=Hkv, d_head=d)
+    with pytest.raises(RuntimeError, match="no CPU fallback"):
+        swa_fused_attention(**args)
+    with pytest.raises(ValueError):
+        swa_fused_attention(**{**args, "sliding_window": 65})
+
+
 def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(N, "_lib", None)
     monkeypatch.setattr(N, "LIB_PATH", tmp_path / "libmia_attn.so")

@@ -4,6 +4,7 @@ from .attention.attention_decode import attention_decode, scatter_packed_k
 from .attention.attention_decode_mask import gen_attention_decode_mask
 from .attention.attention_segmented_cte import segmented_attention
 from .attention.mixed_batch import mixed_batch_attention
+from .attention.swa_fused import swa_fused_attention
 
 __all__ = [
     "flash_attention",
@@ -12,4 +13,5 @@ __all__ = [
     "segmented_attention",
     "scatter_packed_k",
     "mixed_batch_attention",
+    "swa_fused_attention",
 ]

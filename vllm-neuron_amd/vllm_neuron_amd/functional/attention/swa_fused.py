@@ -1,0 +1,147 @@
+"""Fused sliding-window attention layer on the MI355X attention path.
+
+Drop-in for ``vllm_neuron/functional/attention/swa_fused.py``:
+``swa_fused_attention`` keeps the reference signature (:223-244) and the
+semantics of its torch path ``_torch_swa_fused_impl`` (:98-220) for one SWA
+layer of a GPT-OSS-style model:
+
+1. ``qkv = hidden @ qkv_weight + qkv_bias`` (columns ``[Q | K | V]``);
+2. half-split RoPE on Q and K (cos/sin given per active token, halves
+   duplicated), Q scaled by ``scale``;
+3. the post-RoPE K and plain V of the active tokens written into the paged
+   cache at token ``s`` -> logical block ``ceil(prior / block_size) +
+   s // block_size``, slot ``s % block_size`` (prior blocks untouched); a
+   packed FP8 cache stores ``clamp(bf16(x) / scale, +-448)`` as e4m3fn, K in
+   the packed ``[nb, Hkv, bs/2, d, 2]`` layout;
+4. causal sliding-window attention over the prior and active tokens with
+   the per-head sink in the softmax denominator; the active K/V enter at
+   full precision, the prior ones dequantized from the cache;
+5. ``out = attn @ op_weight + op_bias``.
+
+Here the projections are library GEMMs (bf16 inputs, fp32 accumulation),
+the cache write is ``mia_kv_write`` (bf16 copy, or the FP8 divide
+convention), and the attention is the dense ``flash_attention`` prefill
+kernel over the last ``sliding_window - 1`` prior tokens (gathered from the
+cache; older ones are outside every query's window) followed by the active
+ones.  e5m2 caches are not supported (the path's caches are bf16 or e4m3fn).
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from ... import _kernels as K
+from ... import _native as N
+from .attention_cte import flash_attention
+
+
+def _rope(x: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
+    """Half-split RoPE (swa_fused.py:76-85): x*cos + [-x2, x1]*sin, fp32."""
+    d = x.shape[-1]
+    x1, x2 = x[..., : d // 2], x[..., d // 2:]
+    return x * cos + torch.cat([-x2, x1], dim=-1) * sin
+
+
+def _prior_window(k_cache: Tensor, v_cache: Tensor, table_row: Tensor, start: int, end: int,
+                  fp8_packed: bool, k_s: float, v_s: float) -> Tuple[Tensor, Tensor]:
+    """K/V of prior tokens [start, end) of one sequence as bf16 ``[n, Hkv, d]``
+    (dequantized for an FP8 cache; swa_fused.py:160-177)."""
+    bs = v_cache.shape[2]
+    idx = torch.arange(start, end, device=table_row.device)
+    blk = table_row[idx // bs].long()
+    off = idx % bs
+    if fp8_packed:
+        kq = k_cache.view(torch.uint8)[blk, :, off // 2, :, off % 2].view(k_cache.dtype)
+        vq = v_cache.view(torch.uint8)[blk, :, off, :].view(v_cache.dtype)
+        return ((kq.float() * k_s).to(torch.bfloat16), (vq.float() * v_s).to(torch.bfloat16))
+    return k_cache[blk, :, off, :].to(torch.bfloat16), v_cache[blk, :, off, :].to(torch.bfloat16)
+
+
+def swa_fused_attention(
+    hidden_states: Tensor,
+    qkv_weight: Tensor,
+    op_weight: Tensor,
+    k_cache: Tensor,
+    v_cache: Tensor,
+    block_tables: Tensor,
+    cos_cache: Tensor,
+    sin_cache: Tensor,
+    sink: Tensor,
+    prior_tokens: Tensor,
+    qkv_bias: Tensor,
+    op_bias: Tensor,
+    scale: float,
+    sliding_window: int,
+    block_size: int,
+    num_q_heads: int,
+    num_kv_heads: int,
+    d_head: int,
+    k_scale: Optional[Tensor] = None,
+    v_scale: Optional[Tensor] = None,
+) -> Tuple[Tensor, Tensor, Tensor]:
+    """One SWA layer: QKV projection, RoPE, cache write, sliding-window
+    attention with sink, output projection (swa_fused.py:223-326).  Returns
+    ``(out [B, S, H], k_cache, v_cache)``, the caches updated in place."""
+    fp8_packed = k_scale is not None and k_cache.dim() == 5 and k_cache.shape[-1] == 2
+    if k_cache.dtype == torch.float8_e5m2:
+        raise NotImplementedError("swa_fused_attention: e5m2 caches are not supported")
+    if k_cache.dtype == torch.float8_e4m3fn and not fp8_packed:
+        raise NotImplementedError("swa_fused_attention: FP8 caches use the packed K layout")
+    if sliding_window < 1 or sliding_window > block_size:
+        raise ValueError("sliding_window must be in [1, block_size]")
+    if num_q_heads % num_kv_heads:
+        raise ValueError("num_q_heads must be a multiple of num_kv_heads")
+    B, S, H = hidden_states.shape
+    dev = hidden_states.device
+    N.require_gpu(hidden_states, k_cache, v_cache, block_tables)
+    q_dim, kv_dim = num_q_heads * d_head, num_kv_heads * d_head
+    bf = torch.bfloat16
+    k_s = float(k_scale.reshape(-1)[0].item()) if k_scale is not None else 1.0
+    v_s = float(v_scale.reshape(-1)[0].item()) if v_scale is not None else 1.0
+    prior_len = int(prior_tokens.reshape(-1)[0].item())
+    n_prior_blocks = (prior_len + block_size - 1) // block_size
+
+    # 1-2. projection (library GEMM) and RoPE in fp32
+    qkv = torch.addmm(qkv_bias.reshape(1, -1).to(bf), hidden_states.reshape(B * S, H).to(bf),
+                      qkv_weight.to(bf)).float().reshape(B, S, -1)
+    cos = cos_cache.float().unsqueeze(2)
+    sin = sin_cache.float().unsqueeze(2)
+    q = (_rope(qkv[..., :q_dim].reshape(B, S, num_q_heads, d_head), cos, sin) * scale).to(bf)
+    k = _rope(qkv[..., q_dim:q_dim + kv_dim].reshape(B, S, num_kv_heads, d_head), cos, sin).to(bf)
+    v = qkv[..., q_dim + kv_dim:].reshape(B, S, num_kv_heads, d_head).to(bf)
+
+    # only the last sliding_window - 1 prior tokens can be seen by a query
+    p0 = max(0, prior_len - (sliding_window - 1))
+    s_idx = torch.arange(S, device=dev)
+    attn = torch.empty((B, S, num_q_heads, d_head), dtype=bf, device=dev)
+    for b in range(B):
+        row = block_tables[b]
+        # 4a. prior window, read before the active rows are written
+        kp = vp = None
+        if prior_len > p0:
+            kp, vp = _prior_window(k_cache, v_cache, row, p0, prior_len, fp8_packed, k_s, v_s)
+        # 3. active K/V into the cache (prior blocks untouched)
+        slots = (row[n_prior_blocks + s_idx // block_size].long() * block_size
+                 + s_idx % block_size)
+        if fp8_packed:
+            K.kv_write(k[b], None, slots, k_cache, None, k_packed=True,
+                       quant_mode=N.QUANT_DIV_F32, k_scale=k_scale.reshape(1).float())
+            K.kv_write(v[b], None, slots, v_cache, None,
+                       quant_mode=N.QUANT_DIV_F32, k_scale=v_scale.reshape(1).float())
+        else:
+            K.kv_write(k[b], v[b], slots, k_cache, v_cache)
+        # 4b. sliding-window attention, sink in the denominator
+        kw = {}
+        if kp is not None:
+            kw = dict(k_prior=kp.transpose(0, 1), v_prior=vp.transpose(0, 1),
+                      prior_used_len=torch.tensor([prior_len - p0], device=dev))
+        o = flash_attention(q[b].transpose(0, 1), k[b].transpose(0, 1), v[b].transpose(0, 1),
+                            scale=1.0, causal_mask=True, sliding_window=sliding_window,
+                            sink=sink[b].reshape(num_q_heads, 1).float(), tp_k=True, **kw)
+        attn[b] = o.transpose(0, 1)
+    # 5. output projection
+    out = torch.addmm(op_bias.reshape(1, -1).to(bf), attn.reshape(B * S, q_dim),
+                      op_weight.to(bf)).reshape(B, S, H)
+    return out.to(hidden_states.dtype), k_cache, v_cache
