@@ -206,8 +206,8 @@ typedef struct {
   const void *k_cache;
   const void *v_cache;
   int32_t cache_dtype; /* BF16 or FP8_E4M3FN */
-  int32_t k_packed;
-  int64_t k_cache_stride[5];
+  int32_t k_packed;    /* FP8 only: K in the packed layout, read in place */
+  int64_t k_cache_stride[5]; /* block, head, token (pair if packed), dim, lane */
   int64_t v_cache_stride[4];
   int32_t num_blocks;
   int32_t block_size; /* multiple of 16 */
@@ -281,8 +281,8 @@ typedef struct {
   const void *k_cache;
   const void *v_cache;
   int32_t cache_dtype; /* BF16 or FP8_E4M3FN */
-  int32_t k_packed;
-  int64_t k_cache_stride[5];
+  int32_t k_packed;    /* FP8 only: K in the packed layout, read in place */
+  int64_t k_cache_stride[5]; /* block, head, token (pair if packed), dim, lane */
   int64_t v_cache_stride[4];
   int32_t num_blocks;
   int32_t block_size;

@@ -81,6 +81,8 @@ def _decode_args(**over):
     (dict(quant_mode=1), ValueError, "quantisation"),
     (dict(write_slots=0x10000, write_slot_dtype=N.DTYPE_F32), ValueError, "write slots"),
     (dict(blocks_per_seq=0), ValueError, "empty"),
+    (dict(k_packed=1), ValueError, "packed K needs an fp8 cache"),
+    (dict(k_packed=1, cache_dtype=N.DTYPE_FP8_E4M3FN), ValueError, "pairs contiguous"),
 ])
 def test_decode_validation(over, err, text):
     a = _decode_args(**over)
@@ -115,6 +117,10 @@ def _prefill_args(**over):
     (dict(bound_max=0x10000), "both"),
     (dict(bound_min=0x10000, bound_max=0x10000,
           bound_stride=(ctypes.c_int64 * 2)(-1, 4)), "negative bound"),
+    (dict(k_packed=1), "packed K needs an fp8 cache"),
+    (dict(k_packed=1, cache_dtype=N.DTYPE_FP8_E4M3FN), "pairs contiguous"),
+    (dict(k_packed=1, cache_dtype=N.DTYPE_FP8_E4M3FN,
+          k_cache_stride=(ctypes.c_int64 * 5)(16384, 8192, 264, 2, 1)), "pairs contiguous"),
 ])
 def test_prefill_bounds_validation(over, text):
     a = _prefill_args(**over)

@@ -119,6 +119,32 @@ int mia_decode_mask(const mia_mask_args *a, mia_stream_t stream) {
   return mia::launch_decode_mask(*a, (hipStream_t)stream);
 }
 
+// K/V cache layout of the attention kernels: d contiguous, vector-aligned
+// strides (16 bytes for bf16, 8 for fp8); a packed FP8 K cache
+// [nb, Hkv, bs/2, d, 2] has dim stride 2, lane stride 1 and 16-byte
+// aligned block, head and pair strides (its loads are 16 bytes wide).
+static int check_cache_layout(const char *err_dtype, const char *err_layout, int cache_dtype,
+                              int k_packed, int block_size, const void *k, const int64_t *ks,
+                              const void *v, const int64_t *vs) {
+  const bool fp8 = cache_dtype == MIA_DTYPE_FP8_E4M3FN;
+  const int eb = fp8 ? 1 : 2;
+  const size_t vec = fp8 ? 8 : 16;
+  MIA_REQUIRE(!k_packed || fp8, MIA_ERR_VALUE, err_dtype);
+  MIA_REQUIRE(vs[3] == 1 && aligned(v, vec), MIA_ERR_VALUE, err_layout);
+  for (int i = 0; i < 3; ++i)
+    MIA_REQUIRE((vs[i] * eb) % vec == 0, MIA_ERR_VALUE, err_layout);
+  if (k_packed) {
+    MIA_REQUIRE(block_size % 2 == 0 && ks[3] == 2 && ks[4] == 1 && aligned(k, 16) &&
+                    ks[0] % 16 == 0 && ks[1] % 16 == 0 && ks[2] % 16 == 0,
+                MIA_ERR_VALUE, err_layout);
+  } else {
+    MIA_REQUIRE(ks[3] == 1 && aligned(k, vec), MIA_ERR_VALUE, err_layout);
+    for (int i = 0; i < 3; ++i)
+      MIA_REQUIRE((ks[i] * eb) % vec == 0, MIA_ERR_VALUE, err_layout);
+  }
+  return MIA_OK;
+}
+
 static int validate_decode(const mia_decode_args *a) {
   MIA_REQUIRE(a, MIA_ERR_VALUE, "decode: null args");
   MIA_REQUIRE(a->q && a->k_new && a->v_new && a->k_cache && a->v_cache &&
@@ -136,8 +162,6 @@ static int validate_decode(const mia_decode_args *a) {
   MIA_REQUIRE(a->cache_dtype == MIA_DTYPE_BF16 ||
                   a->cache_dtype == MIA_DTYPE_FP8_E4M3FN,
               MIA_ERR_NOT_IMPLEMENTED, "decode: cache dtype must be bf16 or fp8");
-  MIA_REQUIRE(!a->k_packed, MIA_ERR_NOT_IMPLEMENTED,
-              "decode: packed K is read through an unpacked view");
   MIA_REQUIRE(a->block_size > 0 && a->block_size % 16 == 0,
               MIA_ERR_NOT_IMPLEMENTED, "decode: block_size must be a multiple of 16");
   MIA_REQUIRE(a->num_blocks > 0 && a->blocks_per_seq > 0, MIA_ERR_VALUE,
@@ -157,16 +181,15 @@ static int validate_decode(const mia_decode_args *a) {
     MIA_REQUIRE(a->pos_ids, MIA_ERR_VALUE, "decode: pos_ids missing");
   else
     MIA_REQUIRE(a->full_mask, MIA_ERR_VALUE, "decode: mask missing");
-  const int eb = a->cache_dtype == MIA_DTYPE_FP8_E4M3FN ? 1 : 2;
-  const size_t vec = a->cache_dtype == MIA_DTYPE_FP8_E4M3FN ? 8 : 16;
-  MIA_REQUIRE(a->k_cache_stride[3] == 1 && a->v_cache_stride[3] == 1,
-              MIA_ERR_VALUE, "decode: cache head_dim must be contiguous");
-  MIA_REQUIRE(aligned(a->k_cache, vec) && aligned(a->v_cache, vec),
-              MIA_ERR_VALUE, "decode: cache pointers must be vector aligned");
-  for (int i = 0; i < 3; ++i)
-    MIA_REQUIRE(((a->k_cache_stride[i] * eb) % vec == 0) &&
-                    ((a->v_cache_stride[i] * eb) % vec == 0),
-                MIA_ERR_VALUE, "decode: cache strides must be vector aligned");
+  {
+    const int rc = check_cache_layout(
+        "decode: packed K needs an fp8 cache",
+        "decode: cache head_dim must be contiguous (packed K: pairs contiguous) and the "
+        "cache pointers and strides vector aligned",
+        a->cache_dtype, a->k_packed, a->block_size, a->k_cache, a->k_cache_stride, a->v_cache,
+        a->v_cache_stride);
+    if (rc) return rc;
+  }
   MIA_REQUIRE(a->q_stride[3] == 1 && aligned(a->q, 16) &&
                   (a->q_stride[0] * 2) % 16 == 0 && (a->q_stride[1] * 2) % 16 == 0 &&
                   (a->q_stride[2] * 2) % 16 == 0,
@@ -218,23 +241,20 @@ static int validate_prefill(const mia_prefill_args *a) {
   MIA_REQUIRE(a->cache_dtype == MIA_DTYPE_BF16 ||
                   a->cache_dtype == MIA_DTYPE_FP8_E4M3FN,
               MIA_ERR_NOT_IMPLEMENTED, "prefill: cache dtype must be bf16 or fp8");
-  MIA_REQUIRE(!a->k_packed, MIA_ERR_NOT_IMPLEMENTED,
-              "prefill: packed K is read through an unpacked view");
   MIA_REQUIRE(a->block_size > 0 && a->num_blocks > 0 && a->blocks_per_seq >= 0,
               MIA_ERR_VALUE, "prefill: bad cache geometry");
   MIA_REQUIRE(a->block_size % 4 == 0, MIA_ERR_NOT_IMPLEMENTED,
               "prefill: block_size must be a multiple of 4");
   MIA_REQUIRE(a->sliding_window >= 0, MIA_ERR_VALUE, "prefill: negative window");
-  const int eb = a->cache_dtype == MIA_DTYPE_FP8_E4M3FN ? 1 : 2;
-  const size_t vec = a->cache_dtype == MIA_DTYPE_FP8_E4M3FN ? 8 : 16;
-  MIA_REQUIRE(a->k_cache_stride[3] == 1 && a->v_cache_stride[3] == 1,
-              MIA_ERR_VALUE, "prefill: cache head_dim must be contiguous");
-  MIA_REQUIRE(aligned(a->k_cache, vec) && aligned(a->v_cache, vec),
-              MIA_ERR_VALUE, "prefill: cache pointers must be vector aligned");
-  for (int i = 0; i < 3; ++i)
-    MIA_REQUIRE(((a->k_cache_stride[i] * eb) % vec == 0) &&
-                    ((a->v_cache_stride[i] * eb) % vec == 0),
-                MIA_ERR_VALUE, "prefill: cache strides must be vector aligned");
+  {
+    const int rc = check_cache_layout(
+        "prefill: packed K needs an fp8 cache",
+        "prefill: cache head_dim must be contiguous (packed K: pairs contiguous) and the "
+        "cache pointers and strides vector aligned",
+        a->cache_dtype, a->k_packed, a->block_size, a->k_cache, a->k_cache_stride, a->v_cache,
+        a->v_cache_stride);
+    if (rc) return rc;
+  }
   MIA_REQUIRE(a->q_stride[2] == 1 && aligned(a->q, 16) &&
                   (a->q_stride[0] * 2) % 16 == 0 && (a->q_stride[1] * 2) % 16 == 0,
               MIA_ERR_VALUE, "prefill: q must be 16-byte aligned with contiguous d");

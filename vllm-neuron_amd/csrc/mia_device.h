@@ -145,6 +145,29 @@ MIA_DEV u32x4_t e4m3fn_x8_to_bf16_scaled(u32x2_t r) {
   return w;
 }
 
+// Packed FP8 K ([.., bs/2, d, 2]): 16 bytes at channel c of token pair
+// (2i, 2i+1) hold channels c..c+7 of both tokens interleaved (c of 2i, c of
+// 2i+1, c+1 of 2i, ...).  The 8 bytes of one token are the even (token 2i,
+// selector 0x06040200) or odd (token 2i+1, 0x07050301) bytes of each dword
+// pair, in channel order.
+constexpr uint32_t kPackedSelEven = 0x06040200u;
+constexpr uint32_t kPackedSelOdd = 0x07050301u;
+MIA_DEV u32x2_t packed_pair_pick(u32x4_t r, uint32_t sel) {
+  return u32x2_t{__builtin_amdgcn_perm(r[1], r[0], sel), __builtin_amdgcn_perm(r[3], r[2], sel)};
+}
+
+// Same bytes from one 8-byte load per lane: lanes 2i (odd = false) and
+// 2i+1 (odd = true) of a quad load channels c..c+3 and c+4..c+7 of their
+// token pair; each keeps its own token's 4 bytes and trades the other
+// token's 4 with its neighbour (DPP quad_perm [1,0,3,2]).  Returns the
+// lane's token at channels c..c+7 in order.  All lanes must be active.
+MIA_DEV u32x2_t packed_pair_trade(u32x2_t r, bool odd, uint32_t sel_own, uint32_t sel_give) {
+  const uint32_t own = __builtin_amdgcn_perm(r[1], r[0], sel_own);
+  const uint32_t give = __builtin_amdgcn_perm(r[1], r[0], sel_give);
+  const uint32_t got = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)give, 0xB1, 0xF, 0xF, false);
+  return odd ? u32x2_t{got, own} : u32x2_t{own, got};
+}
+
 // Quantise one value the way the reference writes an FP8 cache.
 //   MIA_QUANT_MUL_BF16: bf16(x * s) (x, s bf16-exact), clamp +-448, e4m3fn
 //   MIA_QUANT_MUL_F32 : f32(x * s), clamp, e4m3fn

@@ -43,6 +43,7 @@
 // (attention_decode.py:1081-1150) after every split kernel has read the
 // cache.
 #include <algorithm>
+#include <type_traits>
 
 #include "mia_device.h"
 #include "mia_internal.h"
@@ -262,8 +263,10 @@ MIA_DEV int wave_scan_incl(int x, int lane) {
   return x;
 }
 
-template <int D, int NCP, bool FP8>
+// PK: the K cache is in the packed FP8 layout (FP8 only).
+template <int D, int NCP, bool FP8, bool PK>
 __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(DecodeKParams p) {
+  static_assert(FP8 || !PK, "packed K is an FP8 layout");
   constexpr int EB = FP8 ? 1 : 2;      // cache element bytes
   constexpr int KSTEPS = D / 32;
   constexpr int NSUB = kTile / 16;
@@ -272,6 +275,10 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
   constexpr int VPL = kTile / TL;      // V tokens per lane per tile
   using KL = KLoad<FP8>;
   using raw_t = typename KL::raw_t;
+  // K registers: 8 elements of one token, or for packed K 4 channels of
+  // both tokens of the lane's pair (traded with the neighbour lane)
+  using kraw_t = raw_t;
+  constexpr int KSTEP_B = PK ? 64 : 32 * EB;  // bytes between k-steps of one lane
 
   // V tile of each wave, bf16, rows of D elements, 16-byte chunks XOR-
   // swizzled by row (chunk c of token row t at c ^ (t % (D/8))): the writes
@@ -336,7 +343,20 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
   const int g_q = col_ok ? gcol % p.G : 0;
   const int ds = lane % DS;  // PV lane roles
   const int tl = lane / DS;
-  const int k_lane_off = (qcol * (int)p.kc_t + kg * 8) * EB;
+  // packed K: token pair (qcol & ~1) at its even token's offset; lane
+  // parity k_odd loads channels 8 kg + 4 k_odd .. + 3 of both tokens
+  const bool k_odd = qcol & 1;
+  const int k_lane_off = PK ? (qcol & ~1) * (int)p.kc_t + kg * 16 + 8 * k_odd
+                            : (qcol * (int)p.kc_t + kg * 8) * EB;
+  const uint32_t k_sel_own = k_odd ? kPackedSelOdd : kPackedSelEven;
+  const uint32_t k_sel_give = k_odd ? kPackedSelEven : kPackedSelOdd;
+  auto k_bf16 = [&](const kraw_t &r) {
+    if constexpr (PK)
+      return __builtin_bit_cast(
+          bf16x8_t, e4m3fn_x8_to_bf16_scaled(packed_pair_trade(r, k_odd, k_sel_own, k_sel_give)));
+    else
+      return KL::to_bf16(r);
+  };
   const int v_lane_off = (tl * (int)p.vc_t + ds * 8) * EB;
 
   // ---- PV on MFMA: O^T[d, col] += V^T[d, tok] P^T[tok, col] with
@@ -457,7 +477,7 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
     }
     return r;
   };
-  auto issue_k = [&](raw_t (&kr)[NSUB][KSTEPS], const Item &it, const TileRef &r) {
+  auto issue_k = [&](kraw_t (&kr)[NSUB][KSTEPS], const Item &it, const TileRef &r) {
     const uint8_t *kbase = p.k_cache + (int64_t)it.h * p.kc_h * EB;
 #pragma unroll
     for (int st = 0; st < NSUB; ++st) {
@@ -465,7 +485,7 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
                                    (int64_t)(r.tb[st] - r.bi[st] * p.bs) * p.kc_t) * EB;
 #pragma unroll
       for (int ks = 0; ks < KSTEPS; ++ks)
-        kr[st][ks] = KL::load(kp + k_lane_off + ks * 32 * EB);
+        kr[st][ks] = *reinterpret_cast<const kraw_t *>(kp + k_lane_off + ks * KSTEP_B);
     }
   };
   auto issue_v = [&](raw_t (&vr)[VPL], const Item &it, const TileRef &r, int t0) {
@@ -522,7 +542,7 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
   // the next piece reloads them (no wait on a register still being loaded).
   bf16x8_t q_hold[KSTEPS];
   float st_hold = 0.f, kdq_hold = 1.f;
-  raw_t kr[NSUB][KSTEPS];
+  kraw_t kr[NSUB][KSTEPS];
   raw_t vr[VPL];
   {
     const TileRef r0 = tile_ref(cur, first_tile(cur));
@@ -562,7 +582,7 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
         f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks)
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(KL::to_bf16(kr[st][ks]),
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k_bf16(kr[st][ks]),
                                                         q_cur[ks], acc, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) sc[st][i] = acc[i];
@@ -696,6 +716,7 @@ struct CombineParams {
   const void *wslots;
   int wslot_dtype;
   int cache_dtype;
+  int k_packed;              // K cache in the packed FP8 layout
   uint8_t *k_cache_w;
   uint8_t *v_cache_w;
 };
@@ -862,7 +883,10 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(CombineParams c) {
       else slot = ((const int32_t *)c.wslots)[si];
       if (slot < 0 || slot >= max_slot) continue;  // sentinel: skipped
       const int64_t blk = slot / p.bs, off = slot % p.bs;
-      const int64_t kd = blk * p.kc_blk + h * p.kc_h + off * p.kc_t;
+      // packed K: element e of token off at ((off & ~1) * kc_t + 2 e + (off & 1))
+      const int kstep = c.k_packed ? 2 : 1;
+      const int64_t kd = blk * p.kc_blk + h * p.kc_h +
+                         (c.k_packed ? (off & ~1) * p.kc_t + (off & 1) : off * p.kc_t);
       const int64_t vd = blk * p.vc_blk + h * p.vc_h + off * p.vc_t;
 #pragma unroll
       for (int j = 0; j < DPL; ++j) {
@@ -871,7 +895,7 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(CombineParams c) {
           const float ks = c.k_quant ? c.k_quant[c.quant_per_head ? h : 0] : 1.f;
           const float vs = c.v_quant ? c.v_quant[c.quant_per_head ? h : 0] : 1.f;
           const float kx = bf16_bits_to_f32(kraw[k][j]), vx = bf16_bits_to_f32(vraw[k][j]);
-          c.k_cache_w[kd + e] = (uint8_t)(c.quant_mode == MIA_QUANT_NONE
+          c.k_cache_w[kd + kstep * e] = (uint8_t)(c.quant_mode == MIA_QUANT_NONE
                                               ? f32_to_e4m3fn_bits(kx)
                                               : quantize_e4m3fn(kx, ks, c.quant_mode));
           c.v_cache_w[vd + e] = (uint8_t)(c.quant_mode == MIA_QUANT_NONE
@@ -886,18 +910,18 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(CombineParams c) {
   }
 }
 
-template <int D, int NCP, bool FP8>
+template <int D, int NCP, bool FP8, bool PK>
 void launch_split(const DecodeKParams &kp, dim3 grid, hipStream_t s) {
-  hipLaunchKernelGGL((decode_split_kernel<D, NCP, FP8>), grid, dim3(256), 0, s,
+  hipLaunchKernelGGL((decode_split_kernel<D, NCP, FP8, PK>), grid, dim3(256), 0, s,
                      kp);
 }
 
-template <int D, bool FP8>
+template <int D, bool FP8, bool PK = false>
 void launch_split_ncp(int ncp, const DecodeKParams &kp, dim3 grid,
                       hipStream_t s) {
-  if (ncp <= 4) launch_split<D, 4, FP8>(kp, grid, s);
-  else if (ncp <= 8) launch_split<D, 8, FP8>(kp, grid, s);
-  else launch_split<D, 16, FP8>(kp, grid, s);
+  if (ncp <= 4) launch_split<D, 4, FP8, PK>(kp, grid, s);
+  else if (ncp <= 8) launch_split<D, 8, FP8, PK>(kp, grid, s);
+  else launch_split<D, 16, FP8, PK>(kp, grid, s);
 }
 
 }  // namespace
@@ -953,7 +977,8 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
   kp.v_cache = (const uint8_t *)a.v_cache;
   kp.kc_blk = a.k_cache_stride[0];
   kp.kc_h = a.k_cache_stride[1];
-  kp.kc_t = a.k_cache_stride[2];
+  // packed K: the token stride of the even token of a pair
+  kp.kc_t = a.k_packed ? a.k_cache_stride[2] / 2 : a.k_cache_stride[2];
   kp.vc_blk = a.v_cache_stride[0];
   kp.vc_h = a.v_cache_stride[1];
   kp.vc_t = a.v_cache_stride[2];
@@ -1006,10 +1031,12 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
       kp.col0 = cg * 16;
       const int ncp = std::min(16, pl.ncols - kp.col0);
       if (a.head_dim == 128) {
-        if (fp8) launch_split_ncp<128, true>(ncp, kp, grid, s);
+        if (a.k_packed) launch_split_ncp<128, true, true>(ncp, kp, grid, s);
+        else if (fp8) launch_split_ncp<128, true>(ncp, kp, grid, s);
         else launch_split_ncp<128, false>(ncp, kp, grid, s);
       } else {
-        if (fp8) launch_split_ncp<64, true>(ncp, kp, grid, s);
+        if (a.k_packed) launch_split_ncp<64, true, true>(ncp, kp, grid, s);
+        else if (fp8) launch_split_ncp<64, true>(ncp, kp, grid, s);
         else launch_split_ncp<64, false>(ncp, kp, grid, s);
       }
       int rc = check_hip(hipGetLastError(), "decode split launch");
@@ -1048,6 +1075,7 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
   cp.wslots = a.write_slots;
   cp.wslot_dtype = a.write_slot_dtype;
   cp.cache_dtype = a.cache_dtype;
+  cp.k_packed = a.k_packed;
   cp.k_cache_w = (uint8_t *)a.k_cache;
   cp.v_cache_w = (uint8_t *)a.v_cache;
   const dim3 cgrid((unsigned)pl.ncols, (unsigned)a.num_kv_heads, (unsigned)a.batch);

@@ -31,6 +31,7 @@
 // give 0 (:239).  FP8 caches are widened to bf16 (x 2^-8, exact) while
 // staging; the factor is folded into the scales.
 #include <algorithm>
+#include <type_traits>
 
 #include "mia_device.h"
 #include "mia_internal.h"
@@ -293,8 +294,10 @@ struct Chunk8<true> {
 };
 
 
-template <int D, bool FP8>
+// PK: the K cache is in the packed FP8 layout (FP8 only).
+template <int D, bool FP8, bool PK>
 __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
+  static_assert(FP8 || !PK, "packed K is an FP8 layout");
   constexpr int EB = FP8 ? 1 : 2;
   constexpr int KSTEPS = D / 16;       // k-steps of S^T = K Q^T
   constexpr int DBLK = D / 32;         // 32-row blocks of O^T
@@ -364,9 +367,11 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
   const int64_t bt_row = (int64_t)seq * p.bt_s + (int64_t)h * p.bt_h;
 
   // ---- staging roles
-  // K: thread -> key tid/4, chunks (tid%4) + 4*j  (4 lanes cover 64 bytes)
-  const int k_key = tid >> 2;
-  const int k_c0 = tid & 3;
+  // K: thread -> key tid/4, chunks (tid%4) + 4*j  (4 lanes cover 64 bytes);
+  // packed K: thread -> key pair (2 (tid/8), +1), 16-byte chunks (tid%8) +
+  // 8*j of the pair, each 8 channels of both keys
+  const int k_key = PK ? 2 * (tid >> 3) : tid >> 2;
+  const int k_c0 = PK ? tid & 7 : tid & 3;
   // V: thread -> key group vg (keys 4vg..4vg+3), 8-element chunk vdc
   const bool v_role = tid < VTHREADS;
   const int vg = tid & 15;
@@ -390,16 +395,24 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
     return v < 0 ? 0 : (v >= p.nb ? p.nb - 1 : v);
   };
 
-  raw_t kreg[KCPT];
+  constexpr int KREGS = PK ? KCH / 8 : KCPT;
+  using kraw_t = typename std::conditional<PK, u32x4_t, raw_t>::type;
+  kraw_t kreg[KREGS];
   raw_t vreg[4];
   auto load_tile = [&](int kt, int32_t kphys, int32_t vphys) {
     {
       const int key = clampk(kt + k_key);
-      const int off = key - (int)fdiv((uint32_t)key, p.bs_div) * p.bs;
+      // a packed pair starts at its even key (same block: block_size is even)
+      const int off = (key - (int)fdiv((uint32_t)key, p.bs_div) * p.bs) & (PK ? ~1 : ~0);
       const uint8_t *src = p.k_cache + ((int64_t)kphys * p.kc_blk + (int64_t)h * p.kc_h +
                                         (int64_t)off * p.kc_t) * EB;
 #pragma unroll
-      for (int j = 0; j < KCPT; ++j) kreg[j] = CH::load(src + (k_c0 + 4 * j) * 8 * EB);
+      for (int j = 0; j < KREGS; ++j) {
+        if constexpr (PK)
+          kreg[j] = *reinterpret_cast<const u32x4_t *>(src + (k_c0 + 8 * j) * 16);
+        else
+          kreg[j] = CH::load(src + (k_c0 + 4 * j) * 8 * EB);
+      }
     }
     {
       // the 4 keys of a group share a block (block_size % 4 == 0); keys at
@@ -417,8 +430,18 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
   };
   auto store_tile = [&]() {
 #pragma unroll
-    for (int j = 0; j < KCPT; ++j)
-      *reinterpret_cast<u32x4_t *>(&k_lds[k_key * KROW + (k_c0 + 4 * j) * 8]) = CH::bf16(kreg[j]);
+    for (int j = 0; j < KREGS; ++j) {
+      if constexpr (PK) {
+        const int c = (k_c0 + 8 * j) * 8;
+        *reinterpret_cast<u32x4_t *>(&k_lds[k_key * KROW + c]) =
+            e4m3fn_x8_to_bf16_scaled(packed_pair_pick(kreg[j], kPackedSelEven));
+        *reinterpret_cast<u32x4_t *>(&k_lds[(k_key + 1) * KROW + c]) =
+            e4m3fn_x8_to_bf16_scaled(packed_pair_pick(kreg[j], kPackedSelOdd));
+      } else {
+        *reinterpret_cast<u32x4_t *>(&k_lds[k_key * KROW + (k_c0 + 4 * j) * 8]) =
+            CH::bf16(kreg[j]);
+      }
+    }
     if (v_role) {
       u32x4_t w[4];
 #pragma unroll
@@ -1011,7 +1034,8 @@ int launch_paged_prefill(const mia_prefill_args &a, const PrefillPlan &pl, hipSt
   kp.v_cache = (const uint8_t *)a.v_cache;
   kp.kc_blk = a.k_cache_stride[0];
   kp.kc_h = a.k_cache_stride[1];
-  kp.kc_t = a.k_cache_stride[2];
+  // packed K: the token stride of the even token of a pair
+  kp.kc_t = a.k_packed ? a.k_cache_stride[2] / 2 : a.k_cache_stride[2];
   kp.vc_blk = a.v_cache_stride[0];
   kp.vc_h = a.v_cache_stride[1];
   kp.vc_t = a.v_cache_stride[2];
@@ -1056,11 +1080,13 @@ int launch_paged_prefill(const mia_prefill_args &a, const PrefillPlan &pl, hipSt
   if (pl.dma) {
     hipLaunchKernelGGL((prefill_dma_kernel<128>), grid, dim3(kDmaWaves * 64), 0, s, kp);
   } else if (a.head_dim == 128) {
-    if (fp8) hipLaunchKernelGGL((prefill_kernel<128, true>), grid, dim3(256), 0, s, kp);
-    else hipLaunchKernelGGL((prefill_kernel<128, false>), grid, dim3(256), 0, s, kp);
+    if (a.k_packed) hipLaunchKernelGGL((prefill_kernel<128, true, true>), grid, dim3(256), 0, s, kp);
+    else if (fp8) hipLaunchKernelGGL((prefill_kernel<128, true, false>), grid, dim3(256), 0, s, kp);
+    else hipLaunchKernelGGL((prefill_kernel<128, false, false>), grid, dim3(256), 0, s, kp);
   } else {
-    if (fp8) hipLaunchKernelGGL((prefill_kernel<64, true>), grid, dim3(256), 0, s, kp);
-    else hipLaunchKernelGGL((prefill_kernel<64, false>), grid, dim3(256), 0, s, kp);
+    if (a.k_packed) hipLaunchKernelGGL((prefill_kernel<64, true, true>), grid, dim3(256), 0, s, kp);
+    else if (fp8) hipLaunchKernelGGL((prefill_kernel<64, true, false>), grid, dim3(256), 0, s, kp);
+    else hipLaunchKernelGGL((prefill_kernel<64, false, false>), grid, dim3(256), 0, s, kp);
   }
   int rc = check_hip(hipGetLastError(), "prefill launch");
   if (rc || pl.nsplit <= 1) return rc;

@@ -245,13 +245,15 @@ def paged_decode(
     split_tokens: int = 0,
     split_events: Optional[tuple] = None,
     write_slots: Optional[torch.Tensor] = None,
+    k_packed: bool = False,
 ) -> torch.Tensor:
     """Attention of ``q [B, S, Hq, d]`` over the paged prior context plus the
     active rows ``k_new/v_new [B, S, Hkv, d]``; returns ``[B, S, Hq, d]`` bf16.
 
     ``write_slots [B, S]`` (int32/int64) fuses the cache update: the active
     rows are written to those slots after attention has read the cache;
-    slots outside the pool are skipped.
+    slots outside the pool are skipped.  ``k_packed``: ``k_cache`` is the
+    packed FP8 layout ``[nb, Hkv, bs/2, d, 2]``, read as it lies.
     """
     dev = N.require_gpu(q, k_new, v_new, k_cache, v_cache, block_table)
     if block_table.dtype != torch.int32:
@@ -259,7 +261,7 @@ def paged_decode(
     if q.dtype != torch.bfloat16 or k_new.dtype != torch.bfloat16 or v_new.dtype != torch.bfloat16:
         raise NotImplementedError("decode: q and new K/V must be bf16")
     B, S, Hq, d = q.shape
-    ks, hkv, bs, cd, nb = _cache_view(k_cache)
+    ks, hkv, bs, cd, nb = _cache_view(k_cache, packed=k_packed)
     vs, _, _, _, _ = _cache_view(v_cache)
     if tuple(k_new.shape) != (B, S, hkv, d) or tuple(v_new.shape) != (B, S, hkv, d):
         raise ValueError(
@@ -312,7 +314,7 @@ def paged_decode(
     a.k_cache = k_cache.data_ptr()
     a.v_cache = v_cache.data_ptr()
     a.cache_dtype = N.mia_dtype(k_cache.dtype)
-    a.k_packed = 0
+    a.k_packed = 1 if k_packed else 0
     a.k_cache_stride = _arr(ctypes.c_int64, ks)
     a.v_cache_stride = _arr(ctypes.c_int64, vs[:4])
     a.num_blocks = nb
@@ -398,6 +400,7 @@ def paged_prefill(
     bound_min: Optional[torch.Tensor] = None,
     bound_max: Optional[torch.Tensor] = None,
     empty_rows_uniform: bool = False,
+    k_packed: bool = False,
 ) -> torch.Tensor:
     """``q [T, Hq, d]`` (any token/head strides) over paged K/V; sequence i
     owns rows ``cu_seqlens_q[i]:cu_seqlens_q[i+1]`` and table row i.
@@ -411,14 +414,16 @@ def paged_prefill(
     ``q_offset`` added to query positions, per-(token, q head) key bounds
     ``bound_min``/``bound_max`` ``[T, Hq]`` (int32, any strides; key k is
     visible iff bound_min <= k < bound_max), and ``empty_rows_uniform``
-    (a row that sees no key and has no sink averages all keys uniformly)."""
+    (a row that sees no key and has no sink averages all keys uniformly).
+    ``k_packed``: ``k_cache`` is the packed FP8 layout ``[nb, Hkv, bs/2, d,
+    2]``, read as it lies."""
     dev = N.require_gpu(q, cu_seqlens_q, prior_tokens, k_cache, v_cache, block_table)
     if q.dtype != torch.bfloat16:
         raise NotImplementedError("prefill: q must be bf16")
     if block_table.dtype != torch.int32:
         raise ValueError("block table must be int32")
     T, Hq, d = q.shape
-    ks, hkv, bs, cd, nb = _cache_view(k_cache)
+    ks, hkv, bs, cd, nb = _cache_view(k_cache, packed=k_packed)
     vs, _, _, _, _ = _cache_view(v_cache)
     if cd != d:
         raise ValueError(f"head_dim mismatch: q {d}, cache {cd}")
@@ -458,7 +463,7 @@ def paged_prefill(
     a.k_cache = k_cache.data_ptr()
     a.v_cache = v_cache.data_ptr()
     a.cache_dtype = N.mia_dtype(k_cache.dtype)
-    a.k_packed = 0
+    a.k_packed = 1 if k_packed else 0
     a.k_cache_stride = _arr(ctypes.c_int64, ks)
     a.v_cache_stride = _arr(ctypes.c_int64, vs[:4])
     a.num_blocks = nb

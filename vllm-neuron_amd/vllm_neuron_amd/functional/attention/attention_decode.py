@@ -321,8 +321,8 @@ def attention_decode(
         q = _torch_rms_norm_heads(q, rmsnorm_QK_post_rope_eps, rmsnorm_QK_post_rope_W_Q)
         k = _torch_rms_norm_heads(k, rmsnorm_QK_post_rope_eps, rmsnorm_QK_post_rope_W_K)
 
-    # ---- stage 7 (+ stage 8 fused when the K layout is unpacked): HIP
-    fuse_write = update_cache and not fp8_packed
+    # ---- stage 7 (+ stage 8 fused, either K layout): HIP
+    fuse_write = update_cache
     if update_cache:
         assert kv_cache_update_idx is not None, (
             "kv_cache_update_idx must be provided when update_cache=True")
@@ -338,7 +338,7 @@ def attention_decode(
         write_slots=kv_cache_update_idx if fuse_write else None,
     )  # [B, S, Hq, d]
 
-    # ---- stage 8: KV cache update (HIP; separate scatter for packed K)
+    # ---- stage 8: KV cache update (HIP; fused above unless update_cache is off)
     k_rows = k.transpose(1, 2).reshape(B * S_tkg, kv_heads, d_head)
     v_rows = v.transpose(1, 2).reshape(B * S_tkg, kv_heads, d_head)
     if update_cache:
@@ -399,14 +399,11 @@ def paged_decode_core(
         raise NotImplementedError("k_scale/v_scale are only meaningful with an fp8 KV cache")
     if fp8 and V_cache.dtype != K_cache.dtype:
         raise ValueError("K and V caches must share a dtype")
-    if fp8_packed and write_slots is not None:
-        raise NotImplementedError("fused cache update needs the unpacked K layout")
-    k_read = _unswizzle_packed_k(K_cache) if fp8_packed else K_cache
 
     kw = dict(softmax_scale=softmax_scale, sink=sink,
               k_dequant=k_dequant_scale, v_dequant=v_dequant_scale,
               workspace=workspace, split_tokens=split_tokens, split_events=split_events,
-              write_slots=write_slots)
+              write_slots=write_slots, k_packed=fp8_packed)
     if k_scale is not None:
         kw["quant_mode"] = _quant_mode_for(k_new.dtype, k_scale)
         kw["k_quant"] = k_scale
@@ -433,7 +430,7 @@ def paged_decode_core(
                     f"{(S_ctx, B, Hq, S)}, got {tuple(attention_mask.shape)}")
             kw["full_mask"] = attention_mask
             kw["mask_block_len"] = _mask_resize_block_len(block_len, B, Hq, S, S_ctx)
-    return K.paged_decode(q, k_new, v_new, k_read, V_cache, block_table, **kw)
+    return K.paged_decode(q, k_new, v_new, K_cache, V_cache, block_table, **kw)
 
 
 def _write_rows(k_rows, v_rows, slots, K_cache, V_cache, k_scale, v_scale, kv_heads,

@@ -66,16 +66,24 @@ def segmented_attention(
     Nh, S_q, D = q.shape
     if scale is None:
         scale = 1.0 / (D ** 0.5)
-    if fp8_packed:
-        k_cache = _decode_packed_to_unpacked(k_cache)
-    if k_cache.dim() != 4:
-        raise ValueError(
-            f"k_cache must be [num_blocks, num_kv_heads, block_size, D], got {tuple(k_cache.shape)}")
+    if fp8_packed:  # read in place by the kernel: [nb, Hkv, bs/2, D, 2]
+        assert k_cache.shape[-1] == 2, f"packed K last dim must be 2, got {k_cache.shape[-1]}"
+        if k_cache.dim() != 5:
+            raise ValueError(
+                f"packed k_cache must be [num_blocks, num_kv_heads, block_size/2, D, 2], got "
+                f"{tuple(k_cache.shape)}")
+        cache_bs = 2 * k_cache.shape[2]
+    else:
+        if k_cache.dim() != 4:
+            raise ValueError(
+                f"k_cache must be [num_blocks, num_kv_heads, block_size, D], got "
+                f"{tuple(k_cache.shape)}")
+        cache_bs = k_cache.shape[2]
     num_kv_heads = k_cache.shape[1]
     if Nh % num_kv_heads != 0:
         raise ValueError(f"q heads ({Nh}) must be a multiple of kv heads ({num_kv_heads})")
-    if k_cache.shape[2] != block_size:
-        raise ValueError(f"block_size {block_size} does not match the cache ({k_cache.shape[2]})")
+    if cache_bs != block_size:
+        raise ValueError(f"block_size {block_size} does not match the cache ({cache_bs})")
     if q.dtype != torch.bfloat16:
         raise NotImplementedError("segmented_attention: q must be bf16")
     dev = q.device
@@ -94,6 +102,7 @@ def segmented_attention(
         k_dequant=k_dequant_scale,
         v_dequant=v_dequant_scale,
         out=out.transpose(0, 1),
+        k_packed=fp8_packed,
     )
     if tp_out:
         out = out.transpose(1, 2)
