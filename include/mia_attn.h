@@ -78,8 +78,8 @@ int mia_abi_version(void);
 const char *mia_last_error(void);
 /* sizeof() of each argument struct, so bindings can check their layout.
  * which: 0 kv_write, 1 gather, 2 mask, 3 decode, 4 prefill, 5 slot_mapping,
- * 6 packed_k, 7 swa_trim, 8 scatter_rows, 9 stage.  Returns 0 for an unknown
- * index. */
+ * 6 packed_k, 7 swa_trim, 8 scatter_rows, 9 stage, 10 qkv_epilogue,
+ * 11 row_norm.  Returns 0 for an unknown index. */
 size_t mia_args_size(int which);
 
 /* ------------------------------------------------------------------------ */
@@ -467,6 +467,113 @@ typedef struct {
 } mia_stage_args;
 
 int mia_stage_rows(const mia_stage_args *args, mia_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* QKV epilogue: per-head norm, RoPE, Q scale, split and paged cache write   */
+/* of a fused QKV projection (the GEMM itself is a library call).            */
+/* Replaces: qkv.py:311-414 (_torch_qkv_in_kernel_cache_write_impl: RoPE'd  */
+/*           K/V scattered to slot_mapping, FP8 divide-and-clamp),           */
+/*           qkv.py:263-308 and :516-580 (QK norm and RoPE of _torch_qkv_impl),*/
+/*           attention_decode.py:434-509 and :821-890 (stages 3, 4, 6, 6.5),  */
+/*           swa_fused.py:141-190 (RoPE, q * scale, cache write).            */
+/* Row (t, head) of qkv (heads Q[0, Hq) | K[Hq, Hq+Hkv) | V[.., Hq+2Hkv)),    */
+/* pairs j in [0, d/2): half split (x_j, x_{j+d/2}), interleaved              */
+/* (x_2j, x_2j+1); for Q and K heads, in order:                               */
+/*   pre norm   x <- x * rsqrt(mean(x^2) + eps) * gamma + beta (if enabled)   */
+/*   RoPE       y_a = x_a * cos[t, j]      - x_b * sin[t, j]                  */
+/*              y_b = x_b * cos[t, j + co] + x_a * sin[t, j + so]             */
+/*   post norm  as pre                                                       */
+/*   Q only     y <- y * q_scale                                              */
+/* V heads pass through.  bf16_steps = 1 rounds every product and sum of the  */
+/* RoPE to bf16 (the reference's bf16 tensor ops); 0 keeps them in fp32      */
+/* (no contraction).  Each norm rounds its output to bf16, as the reference   */
+/* does; outputs are bf16.  The cache write stores the final K and V rows     */
+/* (bf16 copy, or FP8 by quant_mode, clamped to [fp8_min, fp8_max]) at        */
+/* slots[t]; slots outside [0, num_blocks * block_size) are skipped.          */
+/* ------------------------------------------------------------------------ */
+typedef struct {
+  const void *qkv;          /* bf16, d contiguous */
+  int64_t qkv_stride;       /* elements between tokens */
+  int64_t num_tokens;
+  int32_t num_q_heads;
+  int32_t num_kv_heads;
+  int32_t head_dim;         /* 64 or 128 */
+  int32_t rope_mode;        /* 0 none, 1 half split, 2 interleaved */
+  const float *cos;         /* element (t, j) at t * cos_stride[0] + j * cos_stride[1] */
+  const float *sin;
+  int64_t cos_stride[2];
+  int64_t sin_stride[2];
+  int32_t cos_hi_off;       /* co: 0 or d/2 (half split only) */
+  int32_t sin_hi_off;       /* so: 0 or d/2 (half split only) */
+  int32_t bf16_steps;
+  int32_t norm_pre;         /* bit 0: Q heads, bit 1: K heads */
+  int32_t norm_post;
+  float eps_pre;
+  float eps_post;
+  float q_scale;            /* 1 = none */
+  const float *gamma_pre_q; /* [d] or NULL (= 1); beta NULL = 0 */
+  const float *gamma_pre_k;
+  const float *beta_pre_q;
+  const float *beta_pre_k;
+  const float *gamma_post_q;
+  const float *gamma_post_k;
+  const float *beta_post_q;
+  const float *beta_post_k;
+  void *q_out;              /* bf16, element (t, h, e) at t*s0 + h*s1 + e */
+  int64_t q_out_stride[2];
+  void *k_out;              /* optional bf16 rows, NULL = not written */
+  int64_t k_out_stride[2];
+  void *v_out;
+  int64_t v_out_stride[2];
+  const void *slots;        /* optional [num_tokens]; NULL = no cache write */
+  int32_t slot_dtype;       /* I32 / I64 / U32 */
+  int32_t cache_dtype;      /* BF16 or FP8_E4M3FN */
+  void *k_cache;
+  void *v_cache;
+  int32_t k_packed;         /* FP8 only: K in the packed layout */
+  int32_t block_size;
+  int64_t k_cache_stride[5]; /* block, head, token (pair if packed), dim, lane */
+  int64_t v_cache_stride[4];
+  int32_t num_blocks;
+  int32_t quant_mode;       /* enum mia_quant_mode (FP8 caches) */
+  int32_t scale_per_head;
+  float fp8_min;            /* clamp of the quantised value (-448 / 448 */
+  float fp8_max;            /*   for e4m3fn) */
+  int32_t _pad0;
+  const float *k_scale;
+  const float *v_scale;
+} mia_qkv_epilogue_args;
+
+int mia_qkv_epilogue(const mia_qkv_epilogue_args *args, mia_stream_t stream);
+
+/* ------------------------------------------------------------------------ */
+/* Row norm of the hidden states before the QKV projection                   */
+/* Replaces: attention_decode.py:405-431 (_torch_rms_norm, stage 1),          */
+/*           qkv.py:466-492 (fused residual add, RMS / LayerNorm / RMS       */
+/*           without gamma in _torch_qkv_impl).                              */
+/* x = in + add0 + add1 (each optional, bf16); mode 1 RMS:                   */
+/*   y = x * rsqrt(sum(x^2) / dim_actual + eps) * gamma                       */
+/* mode 2 LayerNorm: y = (x - mean) * rsqrt(var + eps) * gamma + beta        */
+/* (population variance over the row).  fp32 math, bf16 output; gamma /     */
+/* beta NULL = 1 / 0.                                                        */
+/* ------------------------------------------------------------------------ */
+typedef struct {
+  const void *in;           /* bf16 [rows, dim], d contiguous */
+  const void *add0;         /* optional, same shape */
+  const void *add1;
+  int64_t in_stride;        /* elements between rows (shared by in/add0/add1) */
+  void *out;                /* bf16 */
+  int64_t out_stride;
+  int64_t rows;
+  int32_t dim;
+  int32_t dim_actual;       /* divisor of the RMS mean (0 = dim) */
+  int32_t mode;             /* 1 RMS, 2 LayerNorm */
+  float eps;
+  const float *gamma;       /* [dim] or NULL */
+  const float *beta;        /* [dim] or NULL (LayerNorm) */
+} mia_row_norm_args;
+
+int mia_row_norm(const mia_row_norm_args *args, mia_stream_t stream);
 
 #ifdef __cplusplus
 }

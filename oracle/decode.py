@@ -17,31 +17,7 @@ import torch
 from . import mask as M
 from .fp8 import FP8_CLAMP_MAX
 from .packed import swizzle_packed_k, unswizzle_packed_k
-
-
-def _rms(x, eps, w, dim_actual=None):
-    dt = x.dtype
-    xf = x.to(torch.float32)
-    d = dim_actual if dim_actual is not None else x.shape[-1]
-    y = xf * torch.rsqrt(xf.pow(2).sum(-1, keepdim=True) / d + eps)
-    if w is not None:
-        y = y * w.to(torch.float32)
-    return y.to(dt)
-
-
-def _rope(q, k, cos, sin, contiguous):
-    """attention_decode.py:470-509"""
-    cr = cos.permute(1, 2, 0).unsqueeze(1)
-    sr = sin.permute(1, 2, 0).unsqueeze(1)
-    if contiguous:
-        cf, sf = torch.cat([cr, cr], -1), torch.cat([sr, sr], -1)
-        rot = lambda x: torch.cat((-x[..., x.shape[-1] // 2:], x[..., : x.shape[-1] // 2]), -1)
-    else:
-        cf = torch.stack([cr, cr], -1).flatten(-2)
-        sf = torch.stack([sr, sr], -1).flatten(-2)
-        rot = lambda x: torch.stack((-x[..., 1::2], x[..., 0::2]), -1).flatten(-2)
-    cf, sf = cf.to(q.dtype), sf.to(q.dtype)
-    return q * cf + rot(q) * sf, k * cf + rot(k) * sf
+from .qkv import ref_decode_qkv
 
 
 def ref_attention_decode(
@@ -50,6 +26,7 @@ def ref_attention_decode(
     k_scale=None, v_scale=None, fp8_packed=False, W_out=None, bias_out=None,
     bias_qkv=None, cos=None, sin=None, rope_contiguous_layout=True,
     rmsnorm_X_enabled=False, rmsnorm_X_eps=None, rmsnorm_X_gamma=None,
+    qk_pre=None, qk_post=None, X_hidden_dim_actual=None,
 ):
     """attention_decode.py:653-1182 (attention_dp = dcp = 1)."""
     B, S_tkg, H = X.shape
@@ -65,19 +42,14 @@ def ref_attention_decode(
     if active_blocks_table.dim() > 2 and kv_heads > 1:                 # :791-796
         raise NotImplementedError("per-head table with GQA")
 
-    hidden = X
+    # stages 1-6.5 (:800-890): input RMS norm, projection, split, QK norms, RoPE
+    rx = None
     if rmsnorm_X_enabled:
-        hidden = _rms(hidden, rmsnorm_X_eps if rmsnorm_X_eps is not None else 1e-3,
-                      rmsnorm_X_gamma)
-    qkv = hidden @ W_qkv                                                # :809
-    if bias_qkv is not None:
-        qkv = qkv + bias_qkv
-    qe, ke = q_heads * d_head, q_heads * d_head + kv_heads * d_head
-    q = qkv[..., :qe].view(B, S_tkg, q_heads, d_head).transpose(1, 2)
-    k = qkv[..., qe:ke].view(B, S_tkg, kv_heads, d_head).transpose(1, 2)
-    v = qkv[..., ke:].view(B, S_tkg, kv_heads, d_head).transpose(1, 2)
-    if cos is not None and sin is not None:
-        q, k = _rope(q, k, cos, sin, rope_contiguous_layout)
+        rx = (rmsnorm_X_eps if rmsnorm_X_eps is not None else 1e-3, rmsnorm_X_gamma,
+              X_hidden_dim_actual)
+    q, k, v = ref_decode_qkv(X, W_qkv, q_heads, kv_heads, d_head, bias_qkv=bias_qkv,
+                             rmsnorm_X=rx, qk_pre=qk_pre, qk_post=qk_post, cos=cos, sin=sin,
+                             contiguous=rope_contiguous_layout)
 
     # 7a gather (:915-955)
     safe = torch.where(active_blocks_table < 0, torch.zeros_like(active_blocks_table),

@@ -28,8 +28,9 @@ def _layer(B, S, H, Hq, Hkv, d, bs, prior, W, fp8, seed):
         num_kv_heads=Hkv, d_head=d)
     nblk = (prior + bs - 1) // bs + (S + bs - 1) // bs + 1
     nb = B * nblk + 5
-    a["block_tables"] = torch.stack(
-        [torch.randperm(nb - 1, generator=g)[:nblk] + 1 for _ in range(B)]).int()
+    # rows own disjoint blocks, as sequences do (a block written by one row
+    # and read or written by another makes the result depend on row order)
+    a["block_tables"] = (torch.randperm(nb - 1, generator=g)[:B * nblk] + 1).reshape(B, nblk).int()
     if fp8:
         a["k_cache"] = torch.randn(nb, Hkv, bs // 2, d, 2, generator=g).to(torch.float8_e4m3fn)
         a["v_cache"] = torch.randn(nb, Hkv, bs, d, generator=g).to(torch.float8_e4m3fn)

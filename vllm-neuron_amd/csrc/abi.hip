@@ -55,6 +55,8 @@ size_t mia_args_size(int which) {
     case 7: return sizeof(mia_swa_trim_args);
     case 8: return sizeof(mia_scatter_rows_args);
     case 9: return sizeof(mia_stage_args);
+    case 10: return sizeof(mia_qkv_epilogue_args);
+    case 11: return sizeof(mia_row_norm_args);
     default: return 0;
   }
 }
@@ -312,6 +314,68 @@ int mia_stage_rows(const mia_stage_args *a, mia_stream_t stream) {
   MIA_REQUIRE(a->prior_rows == 0 || a->head_dim == 0 || a->prior, MIA_ERR_VALUE,
               "stage: null prior");
   return mia::launch_stage_rows(*a, (hipStream_t)stream);
+}
+
+int mia_qkv_epilogue(const mia_qkv_epilogue_args *a, mia_stream_t stream) {
+  mia::g_last_error.clear();
+  MIA_REQUIRE(a, MIA_ERR_VALUE, "qkv epilogue: null args");
+  MIA_REQUIRE(a->num_tokens >= 0 && a->num_q_heads > 0 && a->num_kv_heads > 0,
+              MIA_ERR_VALUE, "qkv epilogue: bad shape");
+  MIA_REQUIRE(a->head_dim == 64 || a->head_dim == 128, MIA_ERR_NOT_IMPLEMENTED,
+              "qkv epilogue: head_dim must be 64 or 128");
+  const int64_t width = (int64_t)(a->num_q_heads + 2 * a->num_kv_heads) * a->head_dim;
+  MIA_REQUIRE(a->num_tokens <= 1 || a->qkv_stride >= width, MIA_ERR_VALUE,
+              "qkv epilogue: qkv row stride shorter than the heads");
+  MIA_REQUIRE(a->rope_mode >= 0 && a->rope_mode <= 2, MIA_ERR_VALUE,
+              "qkv epilogue: rope_mode must be 0, 1 or 2");
+  MIA_REQUIRE(a->norm_pre >= 0 && a->norm_pre <= 3 && a->norm_post >= 0 && a->norm_post <= 3 &&
+                  a->eps_pre >= 0.f && a->eps_post >= 0.f,
+              MIA_ERR_VALUE, "qkv epilogue: norm flags are bits 0 (Q) and 1 (K), eps >= 0");
+  if (a->rope_mode != 0) {
+    const int half = a->head_dim / 2;
+    MIA_REQUIRE(a->cos && a->sin, MIA_ERR_VALUE, "qkv epilogue: RoPE needs cos and sin");
+    MIA_REQUIRE((a->cos_hi_off == 0 || (a->rope_mode == 1 && a->cos_hi_off == half)) &&
+                    (a->sin_hi_off == 0 || (a->rope_mode == 1 && a->sin_hi_off == half)),
+                MIA_ERR_VALUE,
+                "qkv epilogue: cos/sin second-half offsets are 0, or head_dim/2 in the half split");
+  }
+  if (a->num_tokens == 0) return MIA_OK;
+  MIA_REQUIRE(a->qkv && a->q_out, MIA_ERR_VALUE, "qkv epilogue: null qkv or q_out");
+  if (a->slots) {
+    MIA_REQUIRE(a->k_cache && a->v_cache, MIA_ERR_VALUE, "qkv epilogue: cache write needs both caches");
+    MIA_REQUIRE(a->slot_dtype == MIA_DTYPE_I32 || a->slot_dtype == MIA_DTYPE_I64 ||
+                    a->slot_dtype == MIA_DTYPE_U32,
+                MIA_ERR_VALUE, "qkv epilogue: slots must be int32, int64 or uint32");
+    MIA_REQUIRE(a->cache_dtype == MIA_DTYPE_BF16 || a->cache_dtype == MIA_DTYPE_FP8_E4M3FN,
+                MIA_ERR_NOT_IMPLEMENTED, "qkv epilogue: cache dtype must be bf16 or fp8");
+    MIA_REQUIRE(!a->k_packed || (a->cache_dtype == MIA_DTYPE_FP8_E4M3FN && a->block_size % 2 == 0),
+                MIA_ERR_VALUE, "qkv epilogue: packed K needs an fp8 cache and an even block size");
+    MIA_REQUIRE(a->block_size > 0 && a->num_blocks > 0, MIA_ERR_VALUE,
+                "qkv epilogue: bad cache geometry");
+    MIA_REQUIRE(a->quant_mode >= MIA_QUANT_NONE && a->quant_mode <= MIA_QUANT_DIV_F32,
+                MIA_ERR_VALUE, "qkv epilogue: bad quant mode");
+    MIA_REQUIRE(a->quant_mode == MIA_QUANT_NONE || (a->cache_dtype == MIA_DTYPE_FP8_E4M3FN &&
+                                                    a->k_scale && a->v_scale),
+                MIA_ERR_VALUE, "qkv epilogue: quantisation needs an fp8 cache and both scales");
+    MIA_REQUIRE(a->quant_mode == MIA_QUANT_NONE || a->fp8_min <= a->fp8_max, MIA_ERR_VALUE,
+                "qkv epilogue: fp8_min > fp8_max");
+  }
+  return mia::launch_qkv_epilogue(*a, (hipStream_t)stream);
+}
+
+int mia_row_norm(const mia_row_norm_args *a, mia_stream_t stream) {
+  mia::g_last_error.clear();
+  MIA_REQUIRE(a, MIA_ERR_VALUE, "row norm: null args");
+  MIA_REQUIRE(a->rows >= 0 && a->dim > 0 && a->dim_actual >= 0, MIA_ERR_VALUE,
+              "row norm: bad shape");
+  MIA_REQUIRE(a->mode == 1 || a->mode == 2, MIA_ERR_VALUE, "row norm: mode must be 1 (RMS) or 2 (LayerNorm)");
+  MIA_REQUIRE(a->eps >= 0.f, MIA_ERR_VALUE, "row norm: eps < 0");
+  if (a->rows == 0) return MIA_OK;
+  MIA_REQUIRE(a->in && a->out, MIA_ERR_VALUE, "row norm: null in or out");
+  MIA_REQUIRE(a->rows <= 1 || (a->in_stride >= a->dim && a->out_stride >= a->dim), MIA_ERR_VALUE,
+              "row norm: row strides shorter than the row");
+  MIA_REQUIRE(a->rows < (1ll << 31), MIA_ERR_VALUE, "row norm: too many rows");
+  return mia::launch_row_norm(*a, (hipStream_t)stream);
 }
 
 static void slot_mapping_one(const mia_slot_mapping_args *a, int64_t t) {

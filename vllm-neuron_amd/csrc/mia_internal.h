@@ -30,6 +30,8 @@ int launch_swa_trim(const mia_swa_trim_args &a, hipStream_t s);
 int launch_packed_k(const mia_packed_k_args &a, hipStream_t s);
 int launch_scatter_rows(const mia_scatter_rows_args &a, hipStream_t s);
 int launch_stage_rows(const mia_stage_args &a, hipStream_t s);
+int launch_qkv_epilogue(const mia_qkv_epilogue_args &a, hipStream_t s);
+int launch_row_norm(const mia_row_norm_args &a, hipStream_t s);
 
 // Paged decode: split-K plan shared by the workspace query and the launch.
 struct DecodePlan {

@@ -680,3 +680,214 @@ def stage_rows(rows: torch.Tensor, prior: Optional[torch.Tensor], prior_rows: in
     a.out_rows, a.head_dim, a.out_dim = int(out_rows), D, int(out_dim)
     N.check(N.lib().mia_stage_rows(ctypes.byref(a), N.stream_ptr(dev)), "stage_rows")
     return out
+
+
+# ---------------------------------------------------------------------------
+# QKV epilogue and row norm
+# ---------------------------------------------------------------------------
+ROPE_NONE, ROPE_HALF, ROPE_INTERLEAVED = 0, 1, 2
+
+
+def _table_2d(x: Optional[torch.Tensor], T: int, dev, what: str):
+    """fp32 ``[T, n]`` view of a cos/sin table (any strides)."""
+    if x is None:
+        raise ValueError(f"RoPE needs {what}")
+    if x.dtype != torch.float32:
+        x = x.to(torch.float32)
+    x = x.to(dev)
+    if x.dim() != 2 or x.shape[0] != T:
+        raise ValueError(f"{what} must be a [num_tokens={T}, n] view, got {tuple(x.shape)}")
+    return x
+
+
+def _rows_3d(x: Optional[torch.Tensor], T: int, H: int, d: int, what: str):
+    if x is None:
+        return None
+    if x.dtype != torch.bfloat16 or tuple(x.shape) != (T, H, d) or x.stride(2) != 1:
+        raise ValueError(f"{what} must be a bf16 [{T}, {H}, {d}] view with contiguous d")
+    return x
+
+
+def qkv_epilogue(
+    qkv: torch.Tensor,
+    num_q_heads: int,
+    num_kv_heads: int,
+    head_dim: int,
+    *,
+    rope_mode: int = ROPE_NONE,
+    cos: Optional[torch.Tensor] = None,
+    sin: Optional[torch.Tensor] = None,
+    cos_hi_off: int = 0,
+    sin_hi_off: int = 0,
+    bf16_steps: bool = False,
+    norm_pre: int = 0,
+    eps_pre: float = 1e-6,
+    gamma_pre: tuple = (None, None),
+    beta_pre: tuple = (None, None),
+    norm_post: int = 0,
+    eps_post: float = 1e-6,
+    gamma_post: tuple = (None, None),
+    beta_post: tuple = (None, None),
+    q_scale: float = 1.0,
+    q_out: Optional[torch.Tensor] = None,
+    k_out: Optional[torch.Tensor] = None,
+    v_out: Optional[torch.Tensor] = None,
+    slots: Optional[torch.Tensor] = None,
+    k_cache: Optional[torch.Tensor] = None,
+    v_cache: Optional[torch.Tensor] = None,
+    k_packed: bool = False,
+    quant_mode: int = N.QUANT_NONE,
+    k_scale: Optional[torch.Tensor] = None,
+    v_scale: Optional[torch.Tensor] = None,
+    scale_per_head: bool = False,
+    fp8_min: float = -448.0,
+    fp8_max: float = 448.0,
+):
+    """Per-head norm, RoPE, Q scale and split of a fused projection
+    ``qkv [T, (Hq + 2 Hkv) * d]`` (bf16, any row stride), with the optional
+    paged cache write of the final K / V rows at ``slots [T]``.
+
+    ``cos``/``sin`` are ``[T, n]`` views; pair j of a row uses ``cos[t, j]``
+    and ``cos[t, j + cos_hi_off]`` (same for sin).  ``norm_*`` flags: bit 0
+    Q heads, bit 1 K heads; ``gamma_*``/``beta_*`` are (Q, K) pairs of
+    ``[d]`` vectors or None.  Returns ``(q_out, k_out, v_out)`` (``[T, H,
+    d]`` bf16; K / V None unless given)."""
+    dev = N.require_gpu(qkv)
+    if qkv.dtype != torch.bfloat16 or qkv.dim() != 2 or qkv.stride(1) != 1:
+        raise ValueError("qkv must be a bf16 [num_tokens, width] view with contiguous columns")
+    T = qkv.shape[0]
+    Hq, Hkv, d = int(num_q_heads), int(num_kv_heads), int(head_dim)
+    if qkv.shape[1] != (Hq + 2 * Hkv) * d:
+        raise ValueError(f"qkv width {qkv.shape[1]} != (Hq + 2 Hkv) * d = {(Hq + 2 * Hkv) * d}")
+    if q_out is None:
+        q_out = torch.empty((T, Hq, d), dtype=torch.bfloat16, device=dev)
+    _rows_3d(q_out, T, Hq, d, "q_out")
+    _rows_3d(k_out, T, Hkv, d, "k_out")
+    _rows_3d(v_out, T, Hkv, d, "v_out")
+    keep = []
+    a = N.QkvEpilogueArgs()
+    a.qkv = qkv.data_ptr()
+    a.qkv_stride = qkv.stride(0)
+    a.num_tokens = T
+    a.num_q_heads, a.num_kv_heads, a.head_dim = Hq, Hkv, d
+    a.rope_mode = int(rope_mode)
+    if rope_mode != ROPE_NONE:
+        c = _table_2d(cos, T, dev, "cos")
+        s = _table_2d(sin, T, dev, "sin")
+        half = d // 2
+        for off in (cos_hi_off, sin_hi_off):
+            if off not in (0, half) or (off and rope_mode != ROPE_HALF):
+                raise ValueError("cos/sin second-half offsets are 0, or head_dim/2 in the "
+                                 "half split")
+        if c.shape[1] < half + cos_hi_off or s.shape[1] < half + sin_hi_off:
+            raise ValueError(f"cos/sin tables need {half + cos_hi_off} / {half + sin_hi_off} "
+                             f"columns, got {c.shape[1]} / {s.shape[1]}")
+        keep += [c, s]
+        a.cos, a.sin = c.data_ptr(), s.data_ptr()
+        a.cos_stride = _arr(ctypes.c_int64, list(c.stride()))
+        a.sin_stride = _arr(ctypes.c_int64, list(s.stride()))
+        a.cos_hi_off, a.sin_hi_off = int(cos_hi_off), int(sin_hi_off)
+    a.bf16_steps = 1 if bf16_steps else 0
+    a.norm_pre, a.norm_post = int(norm_pre), int(norm_post)
+    a.eps_pre, a.eps_post = float(eps_pre), float(eps_post)
+    a.q_scale = float(q_scale)
+    for name, vec in (("gamma_pre_q", gamma_pre[0]), ("gamma_pre_k", gamma_pre[1]),
+                      ("beta_pre_q", beta_pre[0]), ("beta_pre_k", beta_pre[1]),
+                      ("gamma_post_q", gamma_post[0]), ("gamma_post_k", gamma_post[1]),
+                      ("beta_post_q", beta_post[0]), ("beta_post_k", beta_post[1])):
+        v = _scale_f32(vec, dev, d, name)
+        if v is not None:
+            keep.append(v)
+            setattr(a, name, v.data_ptr())
+    a.q_out = q_out.data_ptr()
+    a.q_out_stride = _arr(ctypes.c_int64, [q_out.stride(0), q_out.stride(1)])
+    if k_out is not None:
+        a.k_out = k_out.data_ptr()
+        a.k_out_stride = _arr(ctypes.c_int64, [k_out.stride(0), k_out.stride(1)])
+    if v_out is not None:
+        a.v_out = v_out.data_ptr()
+        a.v_out_stride = _arr(ctypes.c_int64, [v_out.stride(0), v_out.stride(1)])
+    if slots is not None:
+        if k_cache is None or v_cache is None:
+            raise ValueError("the cache write needs k_cache and v_cache")
+        N.require_gpu(qkv, slots, k_cache, v_cache)
+        if slots.numel() != T:
+            raise ValueError(f"slots has {slots.numel()} entries, expected {T}")
+        sl = slots.reshape(-1)
+        if not sl.is_contiguous():
+            sl = sl.contiguous()
+        keep.append(sl)
+        ks, hkv, bs, cd, nb = _cache_view(k_cache, packed=k_packed)
+        vs, vh, vbs, vd, vnb = _cache_view(v_cache)
+        if hkv != Hkv or vh != Hkv or cd != d or vd != d or vbs != bs or vnb != nb:
+            raise ValueError("K/V caches do not match the kv heads / head_dim / geometry")
+        if k_cache.dtype != v_cache.dtype:
+            raise ValueError("K and V caches must share a dtype")
+        a.slots = sl.data_ptr()
+        a.slot_dtype = N.mia_dtype(sl.dtype)
+        a.cache_dtype = N.mia_dtype(k_cache.dtype)
+        a.k_cache, a.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
+        a.k_packed = 1 if k_packed else 0
+        a.block_size, a.num_blocks = bs, nb
+        a.k_cache_stride = _arr(ctypes.c_int64, ks)
+        a.v_cache_stride = _arr(ctypes.c_int64, vs[:4])
+        a.quant_mode = int(quant_mode)
+        a.scale_per_head = 1 if scale_per_head else 0
+        a.fp8_min, a.fp8_max = float(fp8_min), float(fp8_max)
+        if quant_mode != N.QUANT_NONE:
+            need = Hkv if scale_per_head else 1
+            kq = _scale_f32(k_scale, dev, need, "k_scale")
+            vq = _scale_f32(v_scale, dev, need, "v_scale")
+            if kq is None or vq is None:
+                raise ValueError("quantised cache write needs k_scale and v_scale")
+            keep += [kq, vq]
+            a.k_scale, a.v_scale = kq.data_ptr(), vq.data_ptr()
+    N.check(N.lib().mia_qkv_epilogue(ctypes.byref(a), N.stream_ptr(dev)), "qkv_epilogue")
+    return q_out, k_out, v_out
+
+
+NORM_RMS, NORM_LAYER = 1, 2
+
+
+def row_norm(x: torch.Tensor, mode: int, eps: float, gamma: Optional[torch.Tensor] = None,
+             beta: Optional[torch.Tensor] = None, *, add0: Optional[torch.Tensor] = None,
+             add1: Optional[torch.Tensor] = None, dim_actual: int = 0) -> torch.Tensor:
+    """RMS (mode 1) or LayerNorm (mode 2) of the rows of ``x (+ add0) (+
+    add1)`` (bf16 ``[..., dim]``, adds rounded to bf16 in order); fp32
+    statistics, bf16 output of the same shape."""
+    dev = N.require_gpu(x)
+    if x.dtype != torch.bfloat16:
+        raise NotImplementedError("row_norm: bf16 input only")
+    shape = x.shape
+    dim = shape[-1]
+    x2 = x.reshape(-1, dim)
+    adds = []
+    for t in (add0, add1):
+        if t is None:
+            adds.append(None)
+            continue
+        if t.dtype != torch.bfloat16 or t.shape != shape:
+            raise ValueError("residual adds must be bf16 with the input's shape")
+        adds.append(t.reshape(-1, dim))
+    if x2.stride(1) != 1 or any(t is not None and t.stride() != x2.stride() for t in adds):
+        x2 = x2.contiguous()
+        adds = [None if t is None else t.contiguous() for t in adds]
+    out = torch.empty(x2.shape, dtype=torch.bfloat16, device=dev)
+    g = _scale_f32(gamma, dev, dim, "gamma")
+    b = _scale_f32(beta, dev, dim, "beta")
+    a = N.RowNormArgs()
+    a.inp = x2.data_ptr()
+    a.add0 = adds[0].data_ptr() if adds[0] is not None else None
+    a.add1 = adds[1].data_ptr() if adds[1] is not None else None
+    a.in_stride = x2.stride(0)
+    a.out = out.data_ptr()
+    a.out_stride = out.stride(0)
+    a.rows = x2.shape[0]
+    a.dim = dim
+    a.dim_actual = int(dim_actual or 0)
+    a.mode = int(mode)
+    a.eps = float(eps)
+    a.gamma = g.data_ptr() if g is not None else None
+    a.beta = b.data_ptr() if b is not None else None
+    N.check(N.lib().mia_row_norm(ctypes.byref(a), N.stream_ptr(dev)), "row_norm")
+    return out.reshape(shape)

@@ -165,9 +165,41 @@ class StageArgs(ctypes.Structure):
     ]
 
 
+class QkvEpilogueArgs(ctypes.Structure):
+    _fields_ = [
+        ("qkv", c_vp), ("qkv_stride", c_i64), ("num_tokens", c_i64),
+        ("num_q_heads", c_i32), ("num_kv_heads", c_i32), ("head_dim", c_i32),
+        ("rope_mode", c_i32), ("cos", c_vp), ("sin", c_vp),
+        ("cos_stride", c_i64 * 2), ("sin_stride", c_i64 * 2),
+        ("cos_hi_off", c_i32), ("sin_hi_off", c_i32), ("bf16_steps", c_i32),
+        ("norm_pre", c_i32), ("norm_post", c_i32), ("eps_pre", c_f32), ("eps_post", c_f32),
+        ("q_scale", c_f32),
+        ("gamma_pre_q", c_vp), ("gamma_pre_k", c_vp), ("beta_pre_q", c_vp), ("beta_pre_k", c_vp),
+        ("gamma_post_q", c_vp), ("gamma_post_k", c_vp), ("beta_post_q", c_vp),
+        ("beta_post_k", c_vp),
+        ("q_out", c_vp), ("q_out_stride", c_i64 * 2), ("k_out", c_vp), ("k_out_stride", c_i64 * 2),
+        ("v_out", c_vp), ("v_out_stride", c_i64 * 2),
+        ("slots", c_vp), ("slot_dtype", c_i32), ("cache_dtype", c_i32),
+        ("k_cache", c_vp), ("v_cache", c_vp), ("k_packed", c_i32), ("block_size", c_i32),
+        ("k_cache_stride", c_i64 * 5), ("v_cache_stride", c_i64 * 4),
+        ("num_blocks", c_i32), ("quant_mode", c_i32), ("scale_per_head", c_i32),
+        ("fp8_min", c_f32), ("fp8_max", c_f32), ("_pad0", c_i32),
+        ("k_scale", c_vp), ("v_scale", c_vp),
+    ]
+
+
+class RowNormArgs(ctypes.Structure):
+    _fields_ = [
+        ("inp", c_vp), ("add0", c_vp), ("add1", c_vp), ("in_stride", c_i64),
+        ("out", c_vp), ("out_stride", c_i64), ("rows", c_i64), ("dim", c_i32),
+        ("dim_actual", c_i32), ("mode", c_i32), ("eps", c_f32), ("gamma", c_vp), ("beta", c_vp),
+    ]
+
+
 ARGS_STRUCTS = {
     0: KvWriteArgs, 1: GatherArgs, 2: MaskArgs, 3: DecodeArgs, 4: PrefillArgs,
     5: SlotMappingArgs, 6: PackedKArgs, 7: SwaTrimArgs, 8: ScatterRowsArgs, 9: StageArgs,
+    10: QkvEpilogueArgs, 11: RowNormArgs,
 }
 
 # Exported symbols (must match include/mia_attn.h).
@@ -176,7 +208,8 @@ EXPORTS = [
     "mia_gather_kv", "mia_decode_mask", "mia_decode_workspace_bytes",
     "mia_paged_decode", "mia_prefill_workspace_bytes", "mia_paged_prefill", "mia_slot_mapping",
     "mia_slot_mapping_host", "mia_remap_null_block", "mia_swa_trim",
-    "mia_packed_k_convert", "mia_scatter_rows", "mia_stage_rows",
+    "mia_packed_k_convert", "mia_scatter_rows", "mia_stage_rows", "mia_qkv_epilogue",
+    "mia_row_norm",
 ]
 
 _lib = None
@@ -193,7 +226,8 @@ def _declare(lib: ctypes.CDLL) -> None:
                      ("mia_decode_mask", MaskArgs), ("mia_paged_decode", DecodeArgs),
                      ("mia_paged_prefill", PrefillArgs), ("mia_slot_mapping", SlotMappingArgs),
                      ("mia_swa_trim", SwaTrimArgs), ("mia_packed_k_convert", PackedKArgs),
-                     ("mia_scatter_rows", ScatterRowsArgs), ("mia_stage_rows", StageArgs)):
+                     ("mia_scatter_rows", ScatterRowsArgs), ("mia_stage_rows", StageArgs),
+                     ("mia_qkv_epilogue", QkvEpilogueArgs), ("mia_row_norm", RowNormArgs)):
         fn = getattr(lib, name)
         fn.argtypes = [P(st), c_vp]
         fn.restype = c_i32

@@ -4,6 +4,7 @@ from .attention.attention_decode import attention_decode, scatter_packed_k
 from .attention.attention_decode_mask import gen_attention_decode_mask
 from .attention.attention_segmented_cte import segmented_attention
 from .attention.mixed_batch import mixed_batch_attention
+from .attention.qkv import qkv_proj
 from .attention.swa_fused import swa_fused_attention
 
 __all__ = [
@@ -13,5 +14,6 @@ __all__ = [
     "segmented_attention",
     "scatter_packed_k",
     "mixed_batch_attention",
+    "qkv_proj",
     "swa_fused_attention",
 ]

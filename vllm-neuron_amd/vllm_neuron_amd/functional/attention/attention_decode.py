@@ -6,11 +6,17 @@ validation and error classes (:1484-1575, :1724-1741), the block-KV cache
 layout and the output layouts (:1163-1182).
 
 What runs where
-  * RMSNorm / QKV projection / RoPE / O projection (stages 1-6, 9 of
-    :653-1182) are torch ops in this wrapper, written like the reference.
+  * Stage 1 (input RMS norm) is the HIP row norm ``mia_row_norm``; stages 2
+    and 9 (QKV and output projections) are library GEMMs (bf16 inputs,
+    fp32 accumulation, bias fused); stages 3-6.5 (head split, QK RMS norm
+    before / after RoPE, RoPE in the half-split or interleaved layout, with
+    the reference's bf16 rounding of each RoPE product and sum) are one
+    HIP epilogue pass ``mia_qkv_epilogue``.
   * The attention core (stages 7a-7g: block-table gather, GQA, mask,
     sink, softmax, PV) is the HIP split-K decode kernel ``mia_paged_decode``.
-  * The KV-cache update (stage 8) is the HIP scatter ``mia_kv_write``.
+  * The KV-cache update (stage 8) is fused into the decode's combine kernel
+    (either K layout), or the HIP scatter ``mia_kv_write`` when
+    ``update_cache`` is off and the quantised rows are returned.
 
 Differences from the reference's torch fallback, all documented:
   * sentinel write slots (< 0 or >= num_blocks*block_size) are skipped
@@ -40,59 +46,6 @@ from .attention_decode_mask import (
 )
 
 _PMAX = 128
-
-
-# ---------------------------------------------------------------------------
-# torch glue for the projection stages (not the hot path)
-# ---------------------------------------------------------------------------
-def _torch_rms_norm(x: Tensor, eps: float, weight: Optional[Tensor],
-                    dim_actual: Optional[int] = None) -> Tensor:
-    """x / sqrt(sum(x^2)/d + eps) * weight in fp32 (attention_decode.py:406-431)."""
-    dt = x.dtype
-    xf = x.to(torch.float32)
-    d = dim_actual if dim_actual is not None else x.shape[-1]
-    var = xf.pow(2).sum(-1, keepdim=True) / d
-    y = xf * torch.rsqrt(var + eps)
-    if weight is not None:
-        y = y * weight.to(torch.float32)
-    return y.to(dt)
-
-
-def _torch_rms_norm_heads(x: Tensor, eps: float, weight: Optional[Tensor]) -> Tensor:
-    """Per-head RMSNorm over d_head (attention_decode.py:434-453)."""
-    dt = x.dtype
-    xf = x.to(torch.float32)
-    y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
-    if weight is not None:
-        y = y * weight.to(torch.float32).view(-1)
-    return y.to(dt)
-
-
-def _rotate_half(x: Tensor) -> Tensor:
-    h = x.shape[-1] // 2
-    return torch.cat((-x[..., h:], x[..., :h]), dim=-1)
-
-
-def _rotate_half_interleaved(x: Tensor) -> Tensor:
-    return torch.stack((-x[..., 1::2], x[..., 0::2]), dim=-1).flatten(-2)
-
-
-def _torch_apply_rope(q: Tensor, k: Tensor, cos: Tensor, sin: Tensor,
-                      rope_contiguous_layout: bool) -> Tuple[Tensor, Tensor]:
-    """RoPE with cos/sin ``[d/2, B, S]`` (attention_decode.py:470-509)."""
-    cos_r = cos.permute(1, 2, 0).unsqueeze(1)
-    sin_r = sin.permute(1, 2, 0).unsqueeze(1)
-    if rope_contiguous_layout:
-        cos_f = torch.cat([cos_r, cos_r], dim=-1)
-        sin_f = torch.cat([sin_r, sin_r], dim=-1)
-        rot = _rotate_half
-    else:
-        cos_f = torch.stack([cos_r, cos_r], dim=-1).flatten(-2)
-        sin_f = torch.stack([sin_r, sin_r], dim=-1).flatten(-2)
-        rot = _rotate_half_interleaved
-    cos_f = cos_f.to(q.dtype)
-    sin_f = sin_f.to(q.dtype)
-    return q * cos_f + rot(q) * sin_f, k * cos_f + rot(k) * sin_f
 
 
 # ---------------------------------------------------------------------------
@@ -299,27 +252,38 @@ def attention_decode(
     nblk = active_blocks_table.shape[-1]
     S_ctx = nblk * block_len
 
-    # ---- stages 1-6: projections in torch
+    # ---- stages 1-6.5: input RMS norm (HIP), projection (library GEMM), then
+    # split, QK norms and RoPE in one HIP epilogue pass
+    if X.dtype != torch.bfloat16:
+        raise NotImplementedError("attention_decode: X must be bf16")
+    T = B * S_tkg
+    bf = torch.bfloat16
     hidden = X
     if rmsnorm_X_enabled:
         eps = rmsnorm_X_eps if rmsnorm_X_eps is not None else 1e-3
-        hidden = _torch_rms_norm(hidden, eps, rmsnorm_X_gamma, X_hidden_dim_actual)
-    qkv = hidden @ W_qkv
+        g = None if rmsnorm_X_gamma is None else rmsnorm_X_gamma.reshape(-1)
+        hidden = K.row_norm(X, K.NORM_RMS, eps, g, dim_actual=X_hidden_dim_actual or 0)
     if bias_qkv is not None:
-        qkv = qkv + bias_qkv
-    q_end = q_heads * d_head
-    k_end = q_end + kv_heads * d_head
-    q = qkv[..., :q_end].view(B, S_tkg, q_heads, d_head).transpose(1, 2)
-    k = qkv[..., q_end:k_end].view(B, S_tkg, kv_heads, d_head).transpose(1, 2)
-    v = qkv[..., k_end:].view(B, S_tkg, kv_heads, d_head).transpose(1, 2)
-    if rmsnorm_QK_pre_rope_enabled:
-        q = _torch_rms_norm_heads(q, rmsnorm_QK_pre_rope_eps, rmsnorm_QK_pre_rope_W_Q)
-        k = _torch_rms_norm_heads(k, rmsnorm_QK_pre_rope_eps, rmsnorm_QK_pre_rope_W_K)
+        qkv = torch.addmm(bias_qkv.reshape(1, -1).to(bf), hidden.reshape(T, H), W_qkv.to(bf))
+    else:
+        qkv = torch.mm(hidden.reshape(T, H), W_qkv.to(bf))
+    q = torch.empty((B, S_tkg, q_heads, d_head), dtype=bf, device=X.device)
+    k = torch.empty((B, S_tkg, kv_heads, d_head), dtype=bf, device=X.device)
+    v = torch.empty_like(k)
+    ep = {}
     if cos is not None and sin is not None:
-        q, k = _torch_apply_rope(q, k, cos, sin, rope_contiguous_layout)
+        # [d/2, B, S] tables cast to bf16 as the reference does; token-major views
+        tab = lambda c: c.to(bf).to(torch.float32).reshape(d_head // 2, T).t()
+        ep = dict(rope_mode=K.ROPE_HALF if rope_contiguous_layout else K.ROPE_INTERLEAVED,
+                  cos=tab(cos), sin=tab(sin), bf16_steps=True)
+    if rmsnorm_QK_pre_rope_enabled:
+        ep.update(norm_pre=3, eps_pre=rmsnorm_QK_pre_rope_eps,
+                  gamma_pre=(rmsnorm_QK_pre_rope_W_Q, rmsnorm_QK_pre_rope_W_K))
     if rmsnorm_QK_post_rope_enabled:
-        q = _torch_rms_norm_heads(q, rmsnorm_QK_post_rope_eps, rmsnorm_QK_post_rope_W_Q)
-        k = _torch_rms_norm_heads(k, rmsnorm_QK_post_rope_eps, rmsnorm_QK_post_rope_W_K)
+        ep.update(norm_post=3, eps_post=rmsnorm_QK_post_rope_eps,
+                  gamma_post=(rmsnorm_QK_post_rope_W_Q, rmsnorm_QK_post_rope_W_K))
+    K.qkv_epilogue(qkv, q_heads, kv_heads, d_head, q_out=q.view(T, q_heads, d_head),
+                   k_out=k.view(T, kv_heads, d_head), v_out=v.view(T, kv_heads, d_head), **ep)
 
     # ---- stage 7 (+ stage 8 fused, either K layout): HIP
     fuse_write = update_cache
@@ -327,8 +291,7 @@ def attention_decode(
         assert kv_cache_update_idx is not None, (
             "kv_cache_update_idx must be provided when update_cache=True")
     attn = paged_decode_core(
-        q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2),
-        K_cache, V_cache, active_blocks_table,
+        q, k, v, K_cache, V_cache, active_blocks_table,
         block_len=block_len, S_ctx=S_ctx,
         attention_mask=attention_mask, pos_ids=pos_ids,
         swa_start_pos_ids=swa_start_pos_ids, sink=sink,
@@ -339,22 +302,25 @@ def attention_decode(
     )  # [B, S, Hq, d]
 
     # ---- stage 8: KV cache update (HIP; fused above unless update_cache is off)
-    k_rows = k.transpose(1, 2).reshape(B * S_tkg, kv_heads, d_head)
-    v_rows = v.transpose(1, 2).reshape(B * S_tkg, kv_heads, d_head)
+    k_rows = k.reshape(B * S_tkg, kv_heads, d_head)
+    v_rows = v.reshape(B * S_tkg, kv_heads, d_head)
     if update_cache:
         if not fuse_write:
             _write_rows(k_rows, v_rows, kv_cache_update_idx, K_cache, V_cache,
                         k_scale, v_scale, kv_heads, fp8_packed)
         K_out = V_out = None
     else:
-        K_out, V_out = _new_kv_for_return(k, v, k_rows, v_rows, K_cache, k_scale,
+        K_out, V_out = _new_kv_for_return(k.transpose(1, 2), v.transpose(1, 2), k_rows, v_rows,
+                                          K_cache, k_scale,
                                           v_scale, kv_heads)
 
-    # ---- stage 9: output projection (torch)
+    # ---- stage 9: output projection (library GEMM)
     if W_out is not None:
-        output = attn.reshape(B * S_tkg, q_heads * d_head) @ W_out
+        a2 = attn.reshape(B * S_tkg, q_heads * d_head)
         if bias_out is not None:
-            output = output + bias_out
+            output = torch.addmm(bias_out.reshape(1, -1).to(a2.dtype), a2, W_out.to(a2.dtype))
+        else:
+            output = a2 @ W_out
     else:
         output = attn.permute(0, 2, 3, 1).contiguous()
     if update_cache:

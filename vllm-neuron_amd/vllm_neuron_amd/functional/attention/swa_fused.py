@@ -18,12 +18,14 @@ layer of a GPT-OSS-style model:
    full precision, the prior ones dequantized from the cache;
 5. ``out = attn @ op_weight + op_bias``.
 
-Here the projections are library GEMMs (bf16 inputs, fp32 accumulation),
-the cache write is ``mia_kv_write`` (bf16 copy, or the FP8 divide
-convention), and the attention is the dense ``flash_attention`` prefill
-kernel over the last ``sliding_window - 1`` prior tokens (gathered from the
-cache; older ones are outside every query's window) followed by the active
-ones.  e5m2 caches are not supported (the path's caches are bf16 or e4m3fn).
+Here the projections are library GEMMs (bf16 inputs, fp32 accumulation);
+RoPE (fp32), the Q scale, the split and the cache write (bf16 copy, or the
+FP8 divide convention into the packed K layout) are one ``mia_qkv_epilogue``
+pass; the attention is the dense ``flash_attention`` prefill kernel over
+the last ``sliding_window - 1`` prior tokens (gathered from the cache before
+the write; older ones are outside every query's window) followed by the
+active ones.  e5m2 caches are not supported (the path's caches are bf16 or
+e4m3fn).
 """
 from __future__ import annotations
 
@@ -35,13 +37,6 @@ from torch import Tensor
 from ... import _kernels as K
 from ... import _native as N
 from .attention_cte import flash_attention
-
-
-def _rope(x: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
-    """Half-split RoPE (swa_fused.py:76-85): x*cos + [-x2, x1]*sin, fp32."""
-    d = x.shape[-1]
-    x1, x2 = x[..., : d // 2], x[..., d // 2:]
-    return x * cos + torch.cat([-x2, x1], dim=-1) * sin
 
 
 def _prior_window(k_cache: Tensor, v_cache: Tensor, table_row: Tensor, start: int, end: int,
@@ -83,7 +78,11 @@ def swa_fused_attention(
 ) -> Tuple[Tensor, Tensor, Tensor]:
     """One SWA layer: QKV projection, RoPE, cache write, sliding-window
     attention with sink, output projection (swa_fused.py:223-326).  Returns
-    ``(out [B, S, H], k_cache, v_cache)``, the caches updated in place."""
+    ``(out [B, S, H], k_cache, v_cache)``, the caches updated in place.
+
+    The rows of ``block_tables`` must not share the blocks they write (the
+    reference walks rows in order; with disjoint active blocks, as sequences
+    have, every order gives its result)."""
     fp8_packed = k_scale is not None and k_cache.dim() == 5 and k_cache.shape[-1] == 2
     if k_cache.dtype == torch.float8_e5m2:
         raise NotImplementedError("swa_fused_attention: e5m2 caches are not supported")
@@ -103,36 +102,39 @@ def swa_fused_attention(
     prior_len = int(prior_tokens.reshape(-1)[0].item())
     n_prior_blocks = (prior_len + block_size - 1) // block_size
 
-    # 1-2. projection (library GEMM) and RoPE in fp32
-    qkv = torch.addmm(qkv_bias.reshape(1, -1).to(bf), hidden_states.reshape(B * S, H).to(bf),
-                      qkv_weight.to(bf)).float().reshape(B, S, -1)
-    cos = cos_cache.float().unsqueeze(2)
-    sin = sin_cache.float().unsqueeze(2)
-    q = (_rope(qkv[..., :q_dim].reshape(B, S, num_q_heads, d_head), cos, sin) * scale).to(bf)
-    k = _rope(qkv[..., q_dim:q_dim + kv_dim].reshape(B, S, num_kv_heads, d_head), cos, sin).to(bf)
-    v = qkv[..., q_dim + kv_dim:].reshape(B, S, num_kv_heads, d_head).to(bf)
-
-    # only the last sliding_window - 1 prior tokens can be seen by a query
+    T = B * S
+    # only the last sliding_window - 1 prior tokens can be seen by a query;
+    # they are read before the active rows are written
     p0 = max(0, prior_len - (sliding_window - 1))
+    priors = [_prior_window(k_cache, v_cache, block_tables[b], p0, prior_len, fp8_packed, k_s,
+                            v_s) if prior_len > p0 else (None, None) for b in range(B)]
+
+    # 1. projection (library GEMM)
+    qkv = torch.addmm(qkv_bias.reshape(1, -1).to(bf), hidden_states.reshape(T, H).to(bf),
+                      qkv_weight.to(bf))
+    # 2-3. RoPE (fp32), q * scale, split, and the active K/V into the cache at
+    # token s -> logical block ceil(prior / bs) + s // bs (prior blocks untouched)
     s_idx = torch.arange(S, device=dev)
+    slots = (block_tables[:, n_prior_blocks + s_idx // block_size].long() * block_size
+             + s_idx % block_size)
+    q = torch.empty((B, S, num_q_heads, d_head), dtype=bf, device=dev)
+    k = torch.empty((B, S, num_kv_heads, d_head), dtype=bf, device=dev)
+    v = torch.empty_like(k)
+    ep = dict(slots=slots.reshape(T), k_cache=k_cache, v_cache=v_cache, k_packed=fp8_packed)
+    if fp8_packed:
+        ep.update(quant_mode=N.QUANT_DIV_F32, k_scale=k_scale.reshape(-1)[:1],
+                  v_scale=v_scale.reshape(-1)[:1])
+    K.qkv_epilogue(qkv, num_q_heads, num_kv_heads, d_head, rope_mode=K.ROPE_HALF,
+                   cos=cos_cache.float().reshape(T, d_head),
+                   sin=sin_cache.float().reshape(T, d_head), cos_hi_off=d_head // 2,
+                   sin_hi_off=d_head // 2, q_scale=scale,
+                   q_out=q.view(T, num_q_heads, d_head), k_out=k.view(T, num_kv_heads, d_head),
+                   v_out=v.view(T, num_kv_heads, d_head), **ep)
+
+    # 4. sliding-window attention, sink in the denominator
     attn = torch.empty((B, S, num_q_heads, d_head), dtype=bf, device=dev)
     for b in range(B):
-        row = block_tables[b]
-        # 4a. prior window, read before the active rows are written
-        kp = vp = None
-        if prior_len > p0:
-            kp, vp = _prior_window(k_cache, v_cache, row, p0, prior_len, fp8_packed, k_s, v_s)
-        # 3. active K/V into the cache (prior blocks untouched)
-        slots = (row[n_prior_blocks + s_idx // block_size].long() * block_size
-                 + s_idx % block_size)
-        if fp8_packed:
-            K.kv_write(k[b], None, slots, k_cache, None, k_packed=True,
-                       quant_mode=N.QUANT_DIV_F32, k_scale=k_scale.reshape(1).float())
-            K.kv_write(v[b], None, slots, v_cache, None,
-                       quant_mode=N.QUANT_DIV_F32, k_scale=v_scale.reshape(1).float())
-        else:
-            K.kv_write(k[b], v[b], slots, k_cache, v_cache)
-        # 4b. sliding-window attention, sink in the denominator
+        kp, vp = priors[b]
         kw = {}
         if kp is not None:
             kw = dict(k_prior=kp.transpose(0, 1), v_prior=vp.transpose(0, 1),
