@@ -198,6 +198,63 @@ def _measured_traffic(kernel: str, workload: str):
     return None
 
 
+def bench_qkv_epilogue(dev, steps: int, warmup: int) -> dict:
+    """The QKV epilogue (RoPE, split, cache write) and the input row norm at
+    their two shapes: a Llama-3-8B decode step (64 tokens, 32q/8kv, d=128,
+    RMS norms of the 4096-wide rows and of the Q / K heads) and a 2048-token
+    prefill chunk (48q/8kv, d=128, fp32 RoPE tables, packed FP8 cache write
+    with the divide convention).  Average launch time by HIP events on the
+    launching stream; algorithmic bytes = rows read + outputs written."""
+    import torch
+    from vllm_neuron_amd import _kernels as K
+    from vllm_neuron_amd import _native as N
+
+    bf = torch.bfloat16
+    g = torch.Generator(device=dev).manual_seed(5)
+    rnd = lambda *sh: torch.randn(*sh, generator=g, device=dev)
+    B, H, Hq, Hkv, d = 64, 4096, 32, 8, 128
+    X, gam = rnd(B, H).to(bf), rnd(H).abs()
+    qkv_d = rnd(B, (Hq + 2 * Hkv) * d).to(bf)
+    cos_d, sin_d = rnd(B, d // 2).clamp(-1, 1), rnd(B, d // 2).clamp(-1, 1)
+    T, Hq2, nb, bs = 2048, 48, 64, 64
+    qkv_p = rnd(T, (Hq2 + 2 * Hkv) * d).to(bf)
+    cos_p, sin_p = rnd(T, d).clamp(-1, 1), rnd(T, d).clamp(-1, 1)
+    kc = torch.zeros(nb, Hkv, bs // 2, d, 2, dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.zeros(nb, Hkv, bs, d, dtype=torch.float8_e4m3fn, device=dev)
+    slots = torch.arange(T, device=dev)
+    sc = torch.full((1,), 0.05, device=dev)
+    q_p = torch.empty(T, Hq2, d, dtype=bf, device=dev)
+    runs = {
+        "row_norm_vec_kernel (64 x 4096, RMS)": (
+            lambda: K.row_norm(X, K.NORM_RMS, 1e-5, gam), B * H * 2 * 2),
+        "qkv_epilogue_kernel<128> (decode, 64 tokens, QK norm + RoPE)": (
+            lambda: K.qkv_epilogue(qkv_d, Hq, Hkv, d, rope_mode=K.ROPE_HALF, cos=cos_d,
+                                   sin=sin_d, bf16_steps=True, norm_pre=3, eps_pre=1e-6),
+            B * (Hq + 2 * Hkv) * d * 2 + B * Hq * d * 2 + B * d * 4 * 2),
+        "qkv_epilogue_kernel<128> (prefill, 2048 tokens, RoPE + packed FP8 write)": (
+            lambda: K.qkv_epilogue(qkv_p, Hq2, Hkv, d, rope_mode=K.ROPE_HALF, cos=cos_p,
+                                   sin=sin_p, cos_hi_off=d // 2, q_out=q_p, slots=slots,
+                                   k_cache=kc, v_cache=vc, k_packed=True,
+                                   quant_mode=N.QUANT_DIV_F32, k_scale=sc, v_scale=sc),
+            T * (Hq2 + 2 * Hkv) * d * 2 + T * Hq2 * d * 2 + T * 2 * Hkv * d + T * d * 4 * 2),
+    }
+    out = {}
+    stream = torch.cuda.current_stream()
+    for name, (fn, nbytes) in runs.items():
+        for _ in range(warmup):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / steps
+        out[name] = {"us_per_call": round(us, 2), "algorithmic_bytes": nbytes,
+                     "GB_s": round(nbytes / (us * 1e-6) / 1e9, 1)}
+    return out
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -211,6 +268,9 @@ def main() -> int:
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="first run a plain device-to-device copy of this many MiB three "
                          "times (the reference kernel for scaling HBM byte counters)")
+    ap.add_argument("--qkv-epilogue", action="store_true",
+                    help="time the QKV epilogue and row norm kernels instead (one JSON line "
+                         "per kernel shape; not the headline metric)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
@@ -223,6 +283,10 @@ def main() -> int:
     from vllm_neuron_amd import _native
 
     _native.lib()
+    if args.qkv_epilogue:
+        for name, rec in bench_qkv_epilogue(dev, args.steps, min(args.warmup, 20)).items():
+            print(json.dumps({"kernel": name, **rec}), flush=True)
+        return 0
     if args.copy_mib > 0:
         src = torch.ones(args.copy_mib << 20, dtype=torch.uint8, device=dev)
         dst = torch.empty_like(src)

@@ -201,3 +201,56 @@ def test_host_slot_mapping_through_abi():
     a.slot_mapping = out.ctypes.data
     assert N.lib().mia_slot_mapping_host(ctypes.byref(a)) == N.MIA_OK
     assert out.tolist() == [702, 703, 960, 961]
+
+
+def _epilogue_args(**over):
+    a = N.QkvEpilogueArgs()
+    a.qkv, a.q_out = 0x10000, 0x20000  # never dereferenced: validation fails first
+    a.qkv_stride, a.num_tokens = 1536, 4
+    a.num_q_heads, a.num_kv_heads, a.head_dim = 8, 2, 128
+    a.q_out_stride = (ctypes.c_int64 * 2)(1024, 128)
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+@pytest.mark.parametrize("over,text", [
+    (dict(head_dim=96), "head_dim"),
+    (dict(qkv_stride=1000), "row stride"),
+    (dict(qkv=0x10008), "16-byte aligned"),
+    (dict(qkv_stride=1540), "16-byte aligned"),
+    (dict(q_out_stride=(ctypes.c_int64 * 2)(1024, 132)), "outputs must be 16-byte"),
+    (dict(rope_mode=3), "rope_mode"),
+    (dict(rope_mode=1), "cos and sin"),
+    (dict(rope_mode=2, cos=0x30000, sin=0x30000, cos_hi_off=64), "offsets"),
+    (dict(norm_pre=4), "norm flags"),
+    (dict(slots=0x40000, slot_dtype=N.DTYPE_I32), "both caches"),
+    (dict(slots=0x40000, slot_dtype=N.DTYPE_I32, k_cache=0x50000, v_cache=0x50000,
+          cache_dtype=N.DTYPE_BF16, k_packed=1, block_size=16, num_blocks=4), "packed K"),
+    (dict(slots=0x40000, slot_dtype=N.DTYPE_I32, k_cache=0x50000, v_cache=0x50000,
+          cache_dtype=N.DTYPE_BF16, block_size=16, num_blocks=4,
+          k_cache_stride=(ctypes.c_int64 * 5)(4096, 2048, 128, 1, 0),
+          v_cache_stride=(ctypes.c_int64 * 4)(4096, 2048, 128, 2)), "head_dim must be contiguous"),
+    (dict(slots=0x40000, slot_dtype=N.DTYPE_I32, k_cache=0x50000, v_cache=0x50000,
+          cache_dtype=N.DTYPE_FP8_E4M3FN, block_size=16, num_blocks=4, quant_mode=3,
+          k_cache_stride=(ctypes.c_int64 * 5)(4096, 2048, 128, 1, 0),
+          v_cache_stride=(ctypes.c_int64 * 4)(4096, 2048, 128, 1)), "both scales"),
+])
+def test_qkv_epilogue_validation(over, text):
+    a = _epilogue_args(**over)
+    with pytest.raises((ValueError, NotImplementedError), match=text):
+        N.check(N.lib().mia_qkv_epilogue(ctypes.byref(a), None), "qkv_epilogue")
+
+
+@pytest.mark.parametrize("over,text", [
+    (dict(mode=3), "mode"), (dict(dim=0), "bad shape"), (dict(eps=-1.0), "eps"),
+    (dict(in_stride=10), "row strides"), (dict(inp=None), "null"),
+])
+def test_row_norm_validation(over, text):
+    a = N.RowNormArgs()
+    a.inp, a.out, a.rows, a.dim, a.mode, a.eps = 0x10000, 0x20000, 3, 64, 1, 1e-5
+    a.in_stride = a.out_stride = 64
+    for k, v in over.items():
+        setattr(a, k, v)
+    with pytest.raises(ValueError, match=text):
+        N.check(N.lib().mia_row_norm(ctypes.byref(a), None), "row_norm")

@@ -167,10 +167,13 @@ def test_epilogue_q_scale_and_clamp_bounds(gpu):
     assert vals.abs().max().item() == 40  # |x| reaches 50 * 3 sigma
 
 
-@pytest.mark.parametrize("mode,adds,dim_actual", [(1, 0, 0), (1, 2, 0), (1, 0, 3000),
-                                                  (2, 0, 0), (2, 2, 0)])
-def test_row_norm_vs_reference(gpu, mode, adds, dim_actual):
-    rows, H = 7, 4096
+@pytest.mark.parametrize("mode,adds,dim_actual,H", [
+    (1, 0, 0, 4096), (1, 2, 0, 4096), (1, 0, 3000, 4096), (2, 0, 0, 4096), (2, 2, 0, 4096),
+    (1, 2, 0, 1000), (2, 0, 0, 1000),      # 1000 = 125 chunks of 8: vector path, partial wave
+    (1, 2, 0, 1002), (2, 2, 0, 1002),      # not a multiple of 8: element path
+    (1, 0, 0, 20480)])                     # beyond the register-resident row: element path
+def test_row_norm_vs_reference(gpu, mode, adds, dim_actual, H):
+    rows = 7
     g = torch.Generator().manual_seed(mode * 10 + adds)
     x = (torch.randn(rows, H, generator=g) * 2 + 0.5).to(bf)
     m = torch.randn(rows, H, generator=g).to(bf) if adds else None

@@ -341,6 +341,16 @@ int mia_qkv_epilogue(const mia_qkv_epilogue_args *a, mia_stream_t stream) {
   }
   if (a->num_tokens == 0) return MIA_OK;
   MIA_REQUIRE(a->qkv && a->q_out, MIA_ERR_VALUE, "qkv epilogue: null qkv or q_out");
+  // rows are read and written 16 bytes at a time
+  MIA_REQUIRE(aligned(a->qkv, 16) && a->qkv_stride % 8 == 0, MIA_ERR_VALUE,
+              "qkv epilogue: qkv must be 16-byte aligned with a row stride of 8 elements");
+  MIA_REQUIRE(aligned(a->q_out, 16) && a->q_out_stride[0] % 8 == 0 && a->q_out_stride[1] % 8 == 0 &&
+                  (!a->k_out || (aligned(a->k_out, 16) && a->k_out_stride[0] % 8 == 0 &&
+                                 a->k_out_stride[1] % 8 == 0)) &&
+                  (!a->v_out || (aligned(a->v_out, 16) && a->v_out_stride[0] % 8 == 0 &&
+                                 a->v_out_stride[1] % 8 == 0)),
+              MIA_ERR_VALUE,
+              "qkv epilogue: q/k/v outputs must be 16-byte aligned with strides of 8 elements");
   if (a->slots) {
     MIA_REQUIRE(a->k_cache && a->v_cache, MIA_ERR_VALUE, "qkv epilogue: cache write needs both caches");
     MIA_REQUIRE(a->slot_dtype == MIA_DTYPE_I32 || a->slot_dtype == MIA_DTYPE_I64 ||
@@ -352,6 +362,22 @@ int mia_qkv_epilogue(const mia_qkv_epilogue_args *a, mia_stream_t stream) {
                 MIA_ERR_VALUE, "qkv epilogue: packed K needs an fp8 cache and an even block size");
     MIA_REQUIRE(a->block_size > 0 && a->num_blocks > 0, MIA_ERR_VALUE,
                 "qkv epilogue: bad cache geometry");
+    // bf16 rows are stored 16 bytes at a time, fp8 rows 8 (packed K: bytes)
+    const bool fp8 = a->cache_dtype == MIA_DTYPE_FP8_E4M3FN;
+    const int64_t eb = fp8 ? 1 : 2;
+    const size_t vec = fp8 ? 8 : 16;
+    const int64_t *ks = a->k_cache_stride, *vs = a->v_cache_stride;
+    bool ok = vs[3] == 1 && aligned(a->v_cache, vec);
+    for (int i = 0; i < 3; ++i) ok = ok && (vs[i] * eb) % (int64_t)vec == 0;
+    if (a->k_packed) {
+      ok = ok && ks[3] == 2 && ks[4] == 1;
+    } else {
+      ok = ok && ks[3] == 1 && aligned(a->k_cache, vec);
+      for (int i = 0; i < 3; ++i) ok = ok && (ks[i] * eb) % (int64_t)vec == 0;
+    }
+    MIA_REQUIRE(ok, MIA_ERR_VALUE,
+                "qkv epilogue: cache head_dim must be contiguous (packed K: dim stride 2, lane "
+                "stride 1) with vector-aligned pointers and strides");
     MIA_REQUIRE(a->quant_mode >= MIA_QUANT_NONE && a->quant_mode <= MIA_QUANT_DIV_F32,
                 MIA_ERR_VALUE, "qkv epilogue: bad quant mode");
     MIA_REQUIRE(a->quant_mode == MIA_QUANT_NONE || (a->cache_dtype == MIA_DTYPE_FP8_E4M3FN &&
