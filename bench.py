@@ -321,13 +321,13 @@ def main() -> int:
             "hbm_frac_of_step": round(value / HBM_PEAK_GBS, 4),
         },
         "roofline": {
-            "kernel": "decode_split_kernel<128, 4, false>",
+            "kernel": "decode_split_kernel<128, 4, false, false>",
             "bound": "hbm",
             "achieved": round(achieved, 2),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": _measured_traffic("decode_split_kernel<128, 4, false>",
+            "traffic": _measured_traffic("decode_split_kernel<128, 4, false, false>",
                                          "llama3_8b_paged_decode_b64_ctx512-8192"),
             "avg_launch_us": round(dec["split_avg_ms"] * 1e3, 2),
             "algorithmic_bytes": dec["split_bytes"],

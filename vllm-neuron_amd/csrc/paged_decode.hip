@@ -239,12 +239,23 @@ MIA_DEV int64_t share_prefix(const DecodeKParams &p, int w) {
   return c;
 }
 
-// First tile of wave w's share when N tiles are spread over W waves.
+// First tile of wave w's share when N tiles are spread over W waves:
+// floor(N * prefix(w) / prefix(W)).  Computed with one fp64 division, which
+// gives the integer floor exactly: N < 2^31 and prefix(W) < 2^15 (weights
+// <= 6, at most 3 * 256 * 4 waves), so the numerator (< 2^46) and the
+// denominator are exact doubles, and a correctly rounded quotient of such
+// integers cannot round up across an integer (that would need denominator *
+// quotient > 2^53).  A 64-bit integer division is a long
+// scalar routine, and the combine kernel evaluates this ~24 times per wave.
 MIA_DEV int64_t share_start(const DecodeKParams &p, int w, int n_tiles, int waves) {
-  return (int64_t)n_tiles * share_prefix(p, w) / share_prefix(p, waves);
+  const double num = (double)n_tiles * (double)share_prefix(p, w);
+  return (int64_t)floor(num / (double)share_prefix(p, waves));
 }
 
-// Wave holding flattened tile x: the last w with share_start(w) <= x.
+// Wave holding flattened tile x: the last w with share_start(w) <= x (a
+// binary search in scalar registers; an fp64 inversion of the weighted
+// prefix measured slower: its vector registers raised the split kernel's
+// spills, 171 -> 188 us on the FP8 long-context decode).
 MIA_DEV int wave_of_tile(const DecodeKParams &p, int64_t x, int n_tiles, int waves) {
   int lo = 0, hi = waves;  // share_start(lo) <= x < share_start(hi) = N
   while (hi - lo > 1) {
