@@ -110,6 +110,7 @@ struct DecodeKParams {
   float *ws_o;   // [B, Hkv, num_splits, nc_tot, D]
   float *ws_ml;  // [B, Hkv, num_splits, nc_tot, 2]
   int *ws_hdr;   // [B + 2]: tile prefix R[0..B], streaming waves W
+  int *ws_cnt;   // [B * Hkv]: pieces of each segment (by the wave with its last tile)
 };
 
 struct RowInfo {
@@ -693,6 +694,11 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
     l_run = wave_sum_xor(l_run, 32);
     const int64_t ws_row = (((int64_t)cur.b * p.Hkv + cur.h) * p.num_splits + cur.j) * p.nc_tot;
     write_partial(oacc, m_run, l_run, ws_row, cur.j);
+    // the segment's piece count, for the combine, from the piece that ends
+    // at the row's attended end (read from LDS here rather than carried in
+    // the piece registers; each column-group launch writes the same value)
+    if (cur.t_hi >= readfirstlane(s_hi[cur.b]) && lane == 0)
+      p.ws_cnt[cur.b * p.Hkv + cur.h] = cur.j + 1;
 
     if (!nxt.valid) break;
     cur = nxt;
@@ -788,15 +794,9 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(CombineParams c) {
   for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
   if (ri.lo < ri.hi) {
     // the pieces of segment (b, h): one per streaming wave that held one of
-    // its tiles (tile prefix and wave count written by the split kernel)
-    const int r0 = p.ws_hdr[b], r1 = p.ws_hdr[b + 1];
-    const int n_tiles = p.ws_hdr[p.B], n_waves = p.ws_hdr[p.B + 1];
-    const int tb = (r1 - r0) / p.Hkv;
-    const int seg0 = r0 + h * tb;
+    // its tiles, counted by the split kernel's wave that held the last one
     const int sp0 = 0;
-    const int sp1 = min(wave_of_tile(p, seg0 + tb - 1, n_tiles, n_waves) -
-                            wave_of_tile(p, seg0, n_tiles, n_waves) + 1,
-                        p.num_splits);
+    const int sp1 = min(p.ws_cnt[b * p.Hkv + h], p.num_splits);
     const int64_t row0 = ((int64_t)b * p.Hkv + h) * p.num_splits;
     for (int s0 = sp0; s0 < sp1; s0 += kSplitBatch) {
       float ms[kSplitBatch], ls[kSplitBatch], os[kSplitBatch][DPL];
@@ -971,7 +971,8 @@ DecodePlan plan_decode(const mia_decode_args &a) {
   o_bytes = (o_bytes + 255) & ~(size_t)255;
   size_t ml_bytes = rows * 2 * sizeof(float);
   ml_bytes = (ml_bytes + 255) & ~(size_t)255;
-  pl.ws_bytes = o_bytes + ml_bytes + ((size_t)a.batch + 2) * sizeof(int32_t);
+  pl.ws_bytes = o_bytes + ml_bytes + ((size_t)a.batch + 2) * sizeof(int32_t) +
+                (size_t)a.batch * a.num_kv_heads * sizeof(int32_t);
   return pl;
 }
 
@@ -1030,6 +1031,7 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
   kp.ws_o = (float *)a.workspace;
   kp.ws_ml = (float *)((char *)a.workspace + o_bytes);
   kp.ws_hdr = (int *)((char *)a.workspace + o_bytes + ml_bytes);
+  kp.ws_cnt = kp.ws_hdr + (a.batch + 2);
 
   const dim3 grid((unsigned)pl.grid);
   if (a.split_event_begin) {
