@@ -5,12 +5,13 @@ of the hot path: the pure-torch fallbacks of vllm-neuron's attention
 functionals and the numpy metadata code of its model runner.  Every function
 cites the reference file:line it follows (paths relative to the reference
 repository root).  It is imported only by ``tests/``,
-``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py``, as
-the checker / CPU baseline; the product path (``vllm_neuron_amd``) never
-imports it.
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py``, to
+check results and to time the CPU path; the product path
+(``vllm_neuron_amd``) never imports it.
 
 Modules
-  decode     _torch_attention_decode_impl stages 7-8 (+ fp32 textbook math)
+  decode     _torch_attention_decode_impl stages 1-9 (+ fp32 textbook math)
+  qkv        _torch_qkv_impl, the in-kernel cache write, decode stages 1-6.5
   mask       gen_attention_decode_mask torch path and its index helpers
   segmented  _torch_segmented_attention_impl (+ fp32 textbook math)
   dense      _torch_attention_impl of flash_attention (+ float64 textbook)
