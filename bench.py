@@ -274,7 +274,7 @@ def main() -> int:
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {args.gpus} is not supported "
-              "(the attention path is single-GPU in this build)", file=sys.stderr)
+              "(the attention path runs on one GPU)", file=sys.stderr)
         return 2
 
     import torch

@@ -232,7 +232,7 @@ def attention_decode(
         raise NotImplementedError("attention_decode reads the standard K cache layout only")
     if attention_dp > 1 or kv_needs_a2a or dcp_size > 1:
         raise NotImplementedError(
-            "attention DP / DCP span several devices; this build is single-GPU")
+            "attention DP / DCP span several devices; this library runs on one GPU")
     assert active_blocks_table is not None, (
         "attention_decode only supports block KV cache "
         "(active_blocks_table must be provided)")
