@@ -197,6 +197,10 @@ MIA_DEV uint3 xcd_tile() {
     rt = k % R;
     g = (k / R) * X + x;
   }
+  // heaviest row tile first: under the causal mask the last rows see the
+  // most keys, and starting them first shortens the tail (2048-token causal
+  // chunk 107 -> 92 us, a chunk after a 16k prior 1064 -> 1040 us)
+  rt = R - 1 - rt;
   uint3 t;
   t.x = rt;
   t.y = g % gridDim.y;
