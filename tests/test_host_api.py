@@ -151,3 +151,58 @@ def test_workload_generation_deterministic_and_byte_count():
     want = (int(ctx.sum()) * Hkv * d * 2 * 2 + Bq * Hq * d * 4 + Bq * Hkv * d * 4
             + int(valid.sum()) * 4)
     assert e == want
+
+
+# ---------------------------------------------------------------------------
+# qkv_proj contract (qkv.py:35-64, :672-1059): argument errors raise before
+# any device work
+# ---------------------------------------------------------------------------
+def _qkv_args():
+    import torch
+    x = torch.zeros(1, 2, 64, dtype=torch.bfloat16)
+    w = torch.zeros(64, (4 + 2 * 2) * 16, dtype=torch.bfloat16)
+    return x, w
+
+
+def test_qkv_proj_rejects_what_the_reference_rejects():
+    import pytest
+    import torch
+    from vllm_neuron_amd.functional import qkv_proj
+    from vllm_neuron_amd.utils.common_types import NormType, QKVWeightLayout, QuantizationType
+    x, w = _qkv_args()
+    cache = torch.zeros(4, 2, 16, 16, dtype=torch.bfloat16)
+    # in-kernel cache write guardrail
+    with pytest.raises(AssertionError, match="passed together"):
+        qkv_proj(x, w, k_cache=cache, use_block_kv=True, slot_mapping=torch.zeros(2),
+                 block_size=16)
+    with pytest.raises(AssertionError, match="use_block_kv=True"):
+        qkv_proj(x, w, k_cache=cache, v_cache=cache)
+    with pytest.raises(AssertionError, match="slot_mapping and block_size"):
+        qkv_proj(x, w, k_cache=cache, v_cache=cache, use_block_kv=True)
+    # QK norm needs the head counts, RMS only
+    with pytest.raises(AssertionError, match="num_q_heads and num_kv_heads"):
+        qkv_proj(x, w, qk_norm_pre_rope_q_norm=NormType.RMS_NORM)
+    with pytest.raises(AssertionError, match="Only RMS_NORM"):
+        qkv_proj(x, w, num_q_heads=4, num_kv_heads=2,
+                 qk_norm_post_rope_q_norm=NormType.LAYER_NORM,
+                 qk_norm_post_rope_k_norm=NormType.RMS_NORM)
+    # unsupported options of this path
+    with pytest.raises(NotImplementedError):
+        qkv_proj(x, w, quantization_type=QuantizationType.STATIC)
+    with pytest.raises(NotImplementedError):
+        qkv_proj(x, w, transpose_k_cache=True)
+    with pytest.raises(NotImplementedError):
+        qkv_proj(x, w, num_q_heads=4, num_kv_heads=2,
+                 qk_norm_pre_rope_q_norm=NormType.RMS_NORM,
+                 qk_norm_pre_rope_k_norm=NormType.RMS_NORM,
+                 qk_norm_pre_rope_gamma_fused_in_rope_caches=True)
+    with pytest.raises(ValueError, match="norm_b"):
+        qkv_proj(x, w, norm_type=NormType.RMS_NORM, norm_b=torch.zeros(1, 64))
+    with pytest.raises(ValueError, match="hidden must be"):
+        qkv_proj(x, w[:32])
+    with pytest.raises(NotImplementedError, match="bf16"):
+        qkv_proj(x.float(), w)
+    # a CPU tensor never falls back to a CPU path
+    with pytest.raises(RuntimeError):
+        qkv_proj(x, w)
+    assert QKVWeightLayout.CONTIGUOUS.name == "CONTIGUOUS"
