@@ -765,7 +765,10 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(CombineParams c) {
   const int s_q = col / p.G;
   const int hq = h * p.G + col % p.G;
 
-  // ---- independent loads: query, active rows, scales, positions
+  // ---- independent loads: piece count, query, active rows, scales,
+  // positions (the count is read whether or not the row has prior keys, so
+  // that it does not wait for the positions; the workspace always holds it)
+  const int n_pieces = p.ws_cnt[b * p.Hkv + h];
   float q[DPL];
   const uint16_t *qp = p.q + b * p.qs_b + (int64_t)s_q * p.qs_s + hq * p.qs_h;
 #pragma unroll
@@ -796,7 +799,7 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(CombineParams c) {
     // the pieces of segment (b, h): one per streaming wave that held one of
     // its tiles, counted by the split kernel's wave that held the last one
     const int sp0 = 0;
-    const int sp1 = min(p.ws_cnt[b * p.Hkv + h], p.num_splits);
+    const int sp1 = min(n_pieces, p.num_splits);
     const int64_t row0 = ((int64_t)b * p.Hkv + h) * p.num_splits;
     for (int s0 = sp0; s0 < sp1; s0 += kSplitBatch) {
       float ms[kSplitBatch], ls[kSplitBatch], os[kSplitBatch][DPL];
