@@ -287,3 +287,16 @@ def test_fp8_cache_codes_widen_exactly(gpu, head_dim):
     out = _run_core(b).float().cpu().view(rows, d)
     want = codes.view(torch.float8_e4m3fn).float().to(torch.bfloat16).float()
     assert torch.equal(out, want)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_rows_without_prior_keys(gpu, fp8):
+    """Contexts of 1-2 tokens: some rows attend to their active token only
+    (no prior key, no partial to merge) next to rows with one prior key."""
+    cfg = _small_cfg(batch=8, ctx_lo=1, ctx_hi=2, fp8=fp8, sink=True, seed=31)
+    b = _make(cfg, gpu)
+    assert (b.pos == 0).any() and (b.pos > 0).any()
+    out = _run_core(b).float().cpu()
+    ref = _fp32(b, cfg.head_dim ** -0.5)
+    err = (out.double() - ref).abs().max().item()
+    assert err <= (TOL_FP8 if fp8 else TOL_BF16), err

@@ -795,17 +795,19 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(CombineParams c) {
   float M = -INFINITY, L = 0.f, acc[DPL];
 #pragma unroll
   for (int j = 0; j < DPL; ++j) acc[j] = 0.f;
-  if (ri.lo < ri.hi) {
+  {
     // the pieces of segment (b, h): one per streaming wave that held one of
-    // its tiles, counted by the split kernel's wave that held the last one
-    const int sp0 = 0;
-    const int sp1 = min(n_pieces, p.num_splits);
+    // its tiles, counted by the split kernel's wave that held the last one.
+    // The first batch is loaded before the positions arrive (indices clamped
+    // into the segment's slots); a row without prior keys merges none.
+    const int sp_ld = max(1, min(n_pieces, p.num_splits));
+    const int sp1 = ri.lo < ri.hi ? sp_ld : 0;
     const int64_t row0 = ((int64_t)b * p.Hkv + h) * p.num_splits;
-    for (int s0 = sp0; s0 < sp1; s0 += kSplitBatch) {
+    for (int s0 = 0; s0 == 0 || s0 < sp1; s0 += kSplitBatch) {
       float ms[kSplitBatch], ls[kSplitBatch], os[kSplitBatch][DPL];
 #pragma unroll
       for (int i = 0; i < kSplitBatch; ++i) {
-        const int sp = min(s0 + i, sp1 - 1);  // in bounds; extras masked below
+        const int sp = min(s0 + i, sp_ld - 1);  // in bounds; extras masked below
         const int64_t r = (row0 + sp) * NC + col;
         ms[i] = p.ws_ml[r * 2];
         ls[i] = p.ws_ml[r * 2 + 1];
