@@ -139,7 +139,7 @@ typedef struct {
   int32_t blocks_per_seq;
   int32_t block_size;
   int32_t head_dim;
-  int32_t _pad0;
+  int32_t num_blocks; /* physical blocks in the pool: ids are clamped to [0, num_blocks) */
   void *out; /* [batch, num_kv_heads, blocks_per_seq*block_size, head_dim] */
 } mia_gather_args;
 

@@ -83,6 +83,9 @@ def _decode_args(**over):
     (dict(blocks_per_seq=0), ValueError, "empty"),
     (dict(k_packed=1), ValueError, "packed K needs an fp8 cache"),
     (dict(k_packed=1, cache_dtype=N.DTYPE_FP8_E4M3FN), ValueError, "pairs contiguous"),
+    (dict(out_stride=(ctypes.c_int64 * 4)(4096, 4096, 1, 32)), ValueError, "out head_dim"),
+    # 1024 rows x 8 kv heads x 2^18 tiles of a 2^23-token context: > 2^31 tiles
+    (dict(batch=1024, blocks_per_seq=1 << 18), ValueError, "2\\^31"),
 ])
 def test_decode_validation(over, err, text):
     a = _decode_args(**over)
@@ -254,3 +257,24 @@ def test_row_norm_validation(over, text):
         setattr(a, k, v)
     with pytest.raises(ValueError, match=text):
         N.check(N.lib().mia_row_norm(ctypes.byref(a), None), "row_norm")
+
+
+def _gather_args(**over):
+    a = N.GatherArgs()
+    a.cache, a.block_table, a.out = 0x10000, 0x10000, 0x10000
+    a.cache_dtype = N.DTYPE_BF16
+    a.cache_stride = (ctypes.c_int64 * 5)(4096, 4096, 128, 1, 0)
+    a.bt_stride = (ctypes.c_int64 * 3)(4, 0, 1)
+    a.batch, a.num_kv_heads, a.blocks_per_seq, a.block_size, a.head_dim = 1, 1, 4, 32, 128
+    a.num_blocks = 8
+    for k, v in over.items():
+        setattr(a, k, v)
+    return a
+
+
+def test_gather_requires_the_pool_size():
+    """The gather clamps table entries into [0, num_blocks), so it needs the
+    pool size; a zero pool is rejected before any launch."""
+    L = N.lib()
+    with pytest.raises(ValueError, match="geometry"):
+        N.check(L.mia_gather_kv(ctypes.byref(_gather_args(num_blocks=0)), None), "gather_kv")

@@ -45,6 +45,39 @@ def test_mask_and_prefill_refuse_cpu_tensors():
                             torch.tensor([0]), 16, 64, 0.125)
 
 
+def _spy_device_check(monkeypatch):
+    seen = []
+
+    def spy(*tensors):
+        seen.extend(t for t in tensors if t is not None)
+        raise RuntimeError("device check reached")
+
+    monkeypatch.setattr(N, "require_gpu", spy)
+    return seen
+
+
+def test_every_kernel_operand_goes_through_the_device_check(monkeypatch):
+    """A tensor whose address reaches a kernel (positions, masks, sink, out,
+    workspace, slots, bounds) is checked for the device before launch, so a
+    host tensor raises instead of handing the GPU a host pointer."""
+    from vllm_neuron_amd import _kernels as K
+    seen = _spy_device_check(monkeypatch)
+    t = {n: torch.zeros(1) for n in ("pos", "start", "am", "fm", "sink", "out", "ws", "slots")}
+    q = torch.zeros(1, 1, 8, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="device check reached"):
+        K.paged_decode(q, q, q, q, q, q, softmax_scale=1.0, pos_ids=t["pos"], start_pos=t["start"],
+                       active_mask=t["am"], full_mask=t["fm"], sink=t["sink"], out=t["out"],
+                       workspace=t["ws"], write_slots=t["slots"])
+    assert all(any(x is y for y in seen) for x in t.values())
+    seen.clear()
+    p = {n: torch.zeros(1) for n in ("sink", "out", "ws", "kvl", "bmin", "bmax")}
+    with pytest.raises(RuntimeError, match="device check reached"):
+        K.paged_prefill(q, q, q, 1, q, q, q, scale=1.0, sink=p["sink"], out=p["out"],
+                        workspace=p["ws"], kv_len=p["kvl"], bound_min=p["bmin"],
+                        bound_max=p["bmax"])
+    assert all(any(x is y for y in seen) for x in p.values())
+
+
 def test_flash_attention_argument_contract():
     """CPU tensors are refused (no fallback); unsupported options raise
     before any device work."""

@@ -104,7 +104,7 @@ int mia_gather_kv(const mia_gather_args *a, mia_stream_t stream) {
   MIA_REQUIRE(a && a->cache && a->block_table && a->out, MIA_ERR_VALUE,
               "gather: null pointer");
   MIA_REQUIRE(a->batch >= 0 && a->num_kv_heads > 0 && a->blocks_per_seq >= 0 &&
-                  a->block_size > 0 && a->head_dim > 0,
+                  a->block_size > 0 && a->head_dim > 0 && a->num_blocks > 0,
               MIA_ERR_VALUE, "gather: bad geometry");
   return mia::launch_gather(*a, (hipStream_t)stream);
 }
@@ -173,6 +173,10 @@ static int validate_decode(const mia_decode_args *a) {
               "decode: table span shorter than the active tokens");
   MIA_REQUIRE(s_ctx < (1ll << 24), MIA_ERR_VALUE,
               "decode: context beyond 2^24 tokens");
+  // the split kernel counts the 32-token tiles of all (row, kv head)
+  // segments in 32-bit integers
+  MIA_REQUIRE((int64_t)a->batch * a->num_kv_heads * ((s_ctx + 31) / 32) < (1ll << 31),
+              MIA_ERR_VALUE, "decode: batch * kv_heads * context tiles beyond 2^31");
   const int G = a->num_q_heads / a->num_kv_heads;
   MIA_REQUIRE(G * a->s_active <= 64 && a->s_active <= 16,
               MIA_ERR_NOT_IMPLEMENTED,
@@ -200,6 +204,7 @@ static int validate_decode(const mia_decode_args *a) {
               "decode: new K/V head_dim must be contiguous");
   MIA_REQUIRE(a->out_dtype == MIA_DTYPE_BF16, MIA_ERR_NOT_IMPLEMENTED,
               "decode: output dtype must be bf16");
+  MIA_REQUIRE(a->out_stride[3] == 1, MIA_ERR_VALUE, "decode: out head_dim must be contiguous");
   if (a->quant_mode != MIA_QUANT_NONE) {
     MIA_REQUIRE(a->cache_dtype == MIA_DTYPE_FP8_E4M3FN && a->k_quant && a->v_quant,
                 MIA_ERR_VALUE,

@@ -103,7 +103,7 @@ MIA_DEV int elem_bytes(int dtype) {
   return dtype == MIA_DTYPE_FP8_E4M3FN ? 1 : (dtype == MIA_DTYPE_F32 ? 4 : 2);
 }
 
-// out[b, h, j*bs + t, e] = cache[max(bt[b,h,j], 0), h, t, e]
+// out[b, h, j*bs + t, e] = cache[clamp(bt[b,h,j], 0, nb - 1), h, t, e]
 __global__ void gather_kernel(mia_gather_args a, int64_t total) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= total) return;
@@ -119,6 +119,7 @@ __global__ void gather_kernel(mia_gather_args a, int64_t total) {
   int32_t blk = a.block_table[b * a.bt_stride[0] + h * a.bt_stride[1] +
                               j * a.bt_stride[2]];
   if (blk < 0) blk = 0;  // the reference clamps -1 to block 0
+  if (blk >= a.num_blocks) blk = a.num_blocks - 1;  // never read past the pool
   int64_t src;
   if (a.k_packed) {
     src = blk * a.cache_stride[0] + h * a.cache_stride[1] +

@@ -52,19 +52,24 @@ namespace mia {
 namespace {
 
 constexpr int kWaves = 4;
-// resident workgroups per CU of the persistent grid: 3 for FP8 caches (half
-// the bytes per token, so more waves are needed to keep HBM busy; measured
-// 237 -> 218 us on a 16-row 32k-token FP8 decode), else 2 (3 measured equal
-// or slower for bf16)
-constexpr int wg_per_cu(int D, bool fp8) { return (void)D, fp8 ? 3 : 2; }
+// resident workgroups per CU of the persistent grid: 2 (8 waves, 256 VGPRs
+// each).  With streaming V loads an FP8 cache no longer needs a third
+// workgroup to keep HBM busy, and at 2 the FP8 kernels do not spill (at 3
+// they were capped at 168 VGPRs and spilled 28-76 bytes per lane): the
+// B=16 32k-token FP8 decode measured 167 us at 3, 150 us at 2.
+constexpr int wg_per_cu(int D, bool fp8) { return (void)D, (void)fp8, 2; }
 constexpr int kTile = 32;  // tokens per wave tile
 constexpr int kPMax = 128;
 constexpr int kMaxMinTiles = 8;        // longest minimum tile range of a streaming wave
 // share weight of a streaming wave by dispatch class (see share_prefix);
-// FP8 measured on the B=16 32k-token decode: {6,5,4} 171, {7,5,4} 169,
-// {8,6,4} 167.3, {8,5,4} 170, {8,6,5} 169.7 us
+// two classes are populated at two workgroups per CU
 constexpr int kClassWeightBf16[3] = {5, 4, 4};
 constexpr int kClassWeightFp8[3] = {8, 6, 4};
+constexpr int kMaxClassWeight = 8;
+constexpr int kMaxDeviceCUs = 1024;  // the weighted prefix stays below 2^22
+static_assert(kMaxClassWeight * 2 * kMaxDeviceCUs * 4 < (1 << 22), "share_start exactness");
+static_assert(kClassWeightBf16[0] <= kMaxClassWeight && kClassWeightFp8[0] <= kMaxClassWeight,
+              "weights are non-increasing, the first is the largest");
 constexpr int kMaxRows = 1024;         // batch rows of the persistent decode
 
 // Compute units of the current device (queried once per device).
@@ -77,7 +82,7 @@ int device_cu_count() {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         n <= 0)
       n = 256;
-    cache[dev] = n;
+    cache[dev] = std::min(n, kMaxDeviceCUs);
   }
   return cache[dev];
 }
@@ -173,12 +178,19 @@ MIA_DEV int64_t seq_to_linear(int64_t pos, int bl) {
 template <bool FP8>
 struct KLoad;
 
+// K/V tiles are read once per call: streaming (nontemporal) loads keep them
+// from displacing reused lines in L2 and the 256 MB memory-side cache.  On
+// the random 8 KiB (block, head) rows of the Llama-3-8B decode a pure read
+// of 1.1 GB measured 6.7 TB/s with them against 5.9 TB/s with plain loads.
+template <typename T>
+MIA_DEV T stream_load(const uint8_t *p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const T *>(p));
+}
+
 template <>
 struct KLoad<false> {
   typedef u32x4_t raw_t;
-  static MIA_DEV raw_t load(const uint8_t *p) {
-    return *reinterpret_cast<const u32x4_t *>(p);
-  }
+  static MIA_DEV raw_t load(const uint8_t *p) { return stream_load<u32x4_t>(p); }
   static MIA_DEV raw_t zero() { return raw_t{0u, 0u, 0u, 0u}; }
   static MIA_DEV bf16x8_t to_bf16(raw_t r) {
     return __builtin_bit_cast(bf16x8_t, r);
@@ -188,9 +200,7 @@ struct KLoad<false> {
 template <>
 struct KLoad<true> {
   typedef u32x2_t raw_t;
-  static MIA_DEV raw_t load(const uint8_t *p) {
-    return *reinterpret_cast<const u32x2_t *>(p);
-  }
+  static MIA_DEV raw_t load(const uint8_t *p) { return stream_load<u32x2_t>(p); }
   static MIA_DEV raw_t zero() { return raw_t{0u, 0u}; }
   // values are x * 2^-8, exact in bf16
   static MIA_DEV bf16x8_t to_bf16(raw_t r) {
@@ -244,12 +254,12 @@ MIA_DEV int64_t share_prefix(const DecodeKParams &p, int w) {
 
 // First tile of wave w's share when N tiles are spread over W waves:
 // floor(N * prefix(w) / prefix(W)).  Computed with one fp64 division, which
-// gives the integer floor exactly: N < 2^31 and prefix(W) < 2^15 (weights
-// <= 6, at most 3 * 256 * 4 waves), so the numerator (< 2^46) and the
+// gives the integer floor exactly: N < 2^31 (the host rejects larger tile
+// counts) and prefix(W) <= kMaxClassWeight * W < 2^22 (W = waves of the
+// persistent grid, bounded below), so the numerator (< 2^53) and the
 // denominator are exact doubles, and a correctly rounded quotient of such
 // integers cannot round up across an integer (that would need denominator *
-// quotient > 2^53).  A 64-bit integer division is a long
-// scalar routine, and the combine kernel evaluates this ~24 times per wave.
+// N > 2^53).  A 64-bit integer division is a long scalar routine.
 MIA_DEV int64_t share_start(const DecodeKParams &p, int w, int n_tiles, int waves) {
   const double num = (double)n_tiles * (double)share_prefix(p, w);
   return (int64_t)floor(num / (double)share_prefix(p, waves));
@@ -372,6 +382,13 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
       return KL::to_bf16(r);
   };
   const int v_lane_off = (tl * (int)p.vc_t + ds * 8) * EB;
+  // K loads: streaming for bf16 (64 of a row's 256 bytes per load); an FP8
+  // row is read in 32-byte quarters by four loads, which stay plain so that
+  // the line is fetched once and served from L2 to the other three
+  auto k_load = [&](const uint8_t *a) {
+    if constexpr (FP8) return *reinterpret_cast<const kraw_t *>(a);
+    else return stream_load<kraw_t>(a);
+  };
 
   // ---- PV on MFMA: O^T[d, col] += V^T[d, tok] P^T[tok, col] with
   // v_mfma_f32_16x16x32_bf16 per 16-d block.  The contraction index k of
@@ -499,7 +516,7 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
                                    (int64_t)(r.tb[st] - r.bi[st] * p.bs) * p.kc_t) * EB;
 #pragma unroll
       for (int ks = 0; ks < KSTEPS; ++ks)
-        kr[st][ks] = *reinterpret_cast<const kraw_t *>(kp + k_lane_off + ks * KSTEP_B);
+        kr[st][ks] = k_load(kp + k_lane_off + ks * KSTEP_B);
     }
   };
   auto issue_v = [&](raw_t (&vr)[VPL], const Item &it, const TileRef &r, int t0) {

@@ -163,6 +163,7 @@ def gather_kv(cache: torch.Tensor, block_table: torch.Tensor, *, k_packed: bool 
     a.blocks_per_seq = nblk
     a.block_size = bs
     a.head_dim = d
+    a.num_blocks = nb
     a.out = out.data_ptr()
     N.check(N.lib().mia_gather_kv(ctypes.byref(a), N.stream_ptr(dev)), "gather_kv")
     return out
@@ -255,12 +256,18 @@ def paged_decode(
     slots outside the pool are skipped.  ``k_packed``: ``k_cache`` is the
     packed FP8 layout ``[nb, Hkv, bs/2, d, 2]``, read as it lies.
     """
-    dev = N.require_gpu(q, k_new, v_new, k_cache, v_cache, block_table)
+    # every tensor whose address reaches a kernel must live on the device
+    dev = N.require_gpu(q, k_new, v_new, k_cache, v_cache, block_table, pos_ids, start_pos,
+                        active_mask, full_mask, sink, out, workspace, write_slots)
     if block_table.dtype != torch.int32:
         raise ValueError("block table must be int32")
     if q.dtype != torch.bfloat16 or k_new.dtype != torch.bfloat16 or v_new.dtype != torch.bfloat16:
         raise NotImplementedError("decode: q and new K/V must be bf16")
     B, S, Hq, d = q.shape
+    if out is not None and (tuple(out.shape) != (B, S, Hq, d) or out.dtype != torch.bfloat16
+                            or out.stride(3) != 1):
+        raise ValueError(f"out must be a [B, S, Hq, d] = {(B, S, Hq, d)} bf16 tensor with "
+                         "contiguous head_dim")
     ks, hkv, bs, cd, nb = _cache_view(k_cache, packed=k_packed)
     vs, _, _, _, _ = _cache_view(v_cache)
     if tuple(k_new.shape) != (B, S, hkv, d) or tuple(v_new.shape) != (B, S, hkv, d):
@@ -417,7 +424,9 @@ def paged_prefill(
     (a row that sees no key and has no sink averages all keys uniformly).
     ``k_packed``: ``k_cache`` is the packed FP8 layout ``[nb, Hkv, bs/2, d,
     2]``, read as it lies."""
-    dev = N.require_gpu(q, cu_seqlens_q, prior_tokens, k_cache, v_cache, block_table)
+    # every tensor whose address reaches a kernel must live on the device
+    dev = N.require_gpu(q, cu_seqlens_q, prior_tokens, k_cache, v_cache, block_table, sink,
+                        out, workspace, kv_len, bound_min, bound_max)
     if q.dtype != torch.bfloat16:
         raise NotImplementedError("prefill: q must be bf16")
     if block_table.dtype != torch.int32:
@@ -432,6 +441,8 @@ def paged_prefill(
         bts = [block_table.stride(0), 0, block_table.stride(1)]
     elif block_table.dim() == 3:
         th, nblk = block_table.shape[1], block_table.shape[2]
+        if th not in (1, hkv):
+            raise ValueError("per-head table head count does not match the cache")
         bts = [block_table.stride(0), block_table.stride(1) if th > 1 else 0, block_table.stride(2)]
     else:
         raise ValueError("block table must be 2D or 3D")
@@ -451,8 +462,8 @@ def paged_prefill(
     vd = _scale_f32(v_dequant, dev, hkv, "v_dequant")
     if out is None:
         out = torch.empty((T, Hq, d), dtype=torch.bfloat16, device=dev)
-    elif tuple(out.shape) != (T, Hq, d) or out.dtype != torch.bfloat16:
-        raise ValueError("out must be a [T, Hq, d] bf16 tensor")
+    elif tuple(out.shape) != (T, Hq, d) or out.dtype != torch.bfloat16 or out.stride(2) != 1:
+        raise ValueError("out must be a [T, Hq, d] bf16 tensor with contiguous head_dim")
     a = N.PrefillArgs()
     a.q = q.data_ptr()
     a.q_stride = _arr(ctypes.c_int64, list(q.stride()))

@@ -145,8 +145,13 @@ def gen_attention_decode_mask(
             raise IndexError(
                 f"index {lin} is out of bounds for dimension 0 with size {s_prior}")
     mask = K.decode_mask(pos_ids, bs, q_head, s_active, s_prior, start_pos, bl)
-    pos_f = pos_ids.detach().reshape(-1).to(torch.float32).contiguous()
-    st_f = None if start_pos is None else start_pos.detach().reshape(-1).to(torch.float32).contiguous()
+    # The descriptor keeps its own copy of the positions (B*S floats): the
+    # mask encodes the positions as they are now, and a caller that later
+    # updates its position buffer in place must not change what the kernel
+    # reads for this mask.
+    copy = lambda t: t.detach().reshape(-1).to(torch.float32, copy=True).contiguous()
+    pos_f = copy(pos_ids)
+    st_f = None if start_pos is None else copy(start_pos)
     mask._mia_desc = _MaskDesc(pos_f, st_f, bs, q_head, s_active, s_prior, mask._version)
     return mask
 
