@@ -259,6 +259,22 @@ typedef struct {
 size_t mia_decode_workspace_bytes(const mia_decode_args *args);
 int mia_paged_decode(const mia_decode_args *args, mia_stream_t stream);
 
+/* Scratch capacity of mia_paged_decode_noalloc per device, in bytes. */
+#define MIA_DECODE_NOALLOC_SCRATCH_BYTES (64u << 20)
+
+/* No counterpart in the reference (its decode takes its scratch from the
+ * torch allocator).  For callers that cannot allocate device memory: code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  Same arguments and kernels as mia_paged_decode, except that the
+ * split-K scratch is a static per-device array of
+ * MIA_DECODE_NOALLOC_SCRATCH_BYTES inside the library (args->workspace and
+ * args->workspace_bytes are ignored).  Allocates nothing.  A call whose plan
+ * needs more scratch (mia_decode_workspace_bytes) is rejected with
+ * MIA_ERR_VALUE before anything is launched.  Every call on one device shares
+ * that device's array: calls that overlap on one GPU (on different streams)
+ * race; calls ordered on one stream do not. */
+int mia_paged_decode_noalloc(const mia_decode_args *args, mia_stream_t stream);
+
 /* ------------------------------------------------------------------------ */
 /* Paged (chunked / segmented) prefill attention, varlen over sequences      */
 /* Replaces: attention_segmented_cte.py:122-246                             */

@@ -278,3 +278,15 @@ def test_gather_requires_the_pool_size():
     L = N.lib()
     with pytest.raises(ValueError, match="geometry"):
         N.check(L.mia_gather_kv(ctypes.byref(_gather_args(num_blocks=0)), None), "gather_kv")
+
+
+def test_noalloc_decode_rejects_plans_beyond_its_static_scratch():
+    """mia_paged_decode_noalloc refuses a call whose split-K plan needs more
+    than MIA_DECODE_NOALLOC_SCRATCH_BYTES, before touching the device."""
+    L = N.lib()
+    a = _decode_args(batch=1024, blocks_per_seq=256)
+    assert L.mia_decode_workspace_bytes(ctypes.byref(a)) > N.DECODE_NOALLOC_SCRATCH_BYTES
+    with pytest.raises(ValueError, match="static scratch"):
+        N.check(L.mia_paged_decode_noalloc(ctypes.byref(a), None), "paged_decode_noalloc")
+    hdr = (ROOT / "include" / "mia_attn.h").read_text()
+    assert f"MIA_DECODE_NOALLOC_SCRATCH_BYTES ({N.DECODE_NOALLOC_SCRATCH_BYTES >> 20}u << 20)" in hdr

@@ -236,6 +236,24 @@ int mia_paged_decode(const mia_decode_args *a, mia_stream_t stream) {
   return mia::launch_paged_decode(*a, pl, (hipStream_t)stream);
 }
 
+int mia_paged_decode_noalloc(const mia_decode_args *a, mia_stream_t stream) {
+  mia::g_last_error.clear();
+  int rc = validate_decode(a);
+  if (rc) return rc;
+  const mia::DecodePlan pl = mia::plan_decode(*a);
+  MIA_REQUIRE(pl.ws_bytes <= MIA_DECODE_NOALLOC_SCRATCH_BYTES, MIA_ERR_VALUE,
+              "decode (no-alloc): the call needs " + std::to_string(pl.ws_bytes) +
+                  " bytes of scratch, the static scratch holds " +
+                  std::to_string((size_t)MIA_DECODE_NOALLOC_SCRATCH_BYTES));
+  void *ws = nullptr;
+  rc = mia::decode_noalloc_scratch(&ws);
+  if (rc) return rc;
+  mia_decode_args b = *a;
+  b.workspace = ws;
+  b.workspace_bytes = MIA_DECODE_NOALLOC_SCRATCH_BYTES;
+  return mia::launch_paged_decode(b, pl, (hipStream_t)stream);
+}
+
 static int validate_prefill(const mia_prefill_args *a) {
   MIA_REQUIRE(a->q && a->cu_seqlens_q && a->prior_tokens && a->k_cache &&
                   a->v_cache && a->block_table && a->out,

@@ -44,6 +44,9 @@ struct DecodePlan {
   size_t ws_bytes;   // workspace bytes
 };
 DecodePlan plan_decode(const mia_decode_args &a);
+// Device address of the current device's static decode scratch
+// (MIA_DECODE_NOALLOC_SCRATCH_BYTES), looked up once per device.
+int decode_noalloc_scratch(void **ptr);
 int launch_paged_decode(const mia_decode_args &a, const DecodePlan &p,
                         hipStream_t s);
 

@@ -43,10 +43,17 @@
 // (attention_decode.py:1081-1150) after every split kernel has read the
 // cache.
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "mia_device.h"
 #include "mia_internal.h"
+
+// Split-K scratch of the allocation-free decode entry point: one copy per
+// device, held until the process ends.  Host code must not pass `scratch`
+// itself to a kernel (in host code the name is only a stand-in for the
+// symbol): its device address comes from hipGetSymbolAddress, per device.
+static __device__ __align__(256) uint8_t scratch[MIA_DECODE_NOALLOC_SCRATCH_BYTES];
 
 namespace mia {
 namespace {
@@ -960,6 +967,27 @@ void launch_split_ncp(int ncp, const DecodeKParams &kp, dim3 grid,
 }
 
 }  // namespace
+
+int decode_noalloc_scratch(void **ptr) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void *addr[kMaxDevices] = {nullptr};
+  int dev = -1;
+  int rc = check_hip(hipGetDevice(&dev), "decode scratch: current device");
+  if (rc) return rc;
+  if (dev < 0 || dev >= kMaxDevices)
+    return set_error(MIA_ERR_RUNTIME, "decode scratch: device index out of range");
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[dev]) {
+    void *p = nullptr;
+    rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "decode scratch: symbol address");
+    if (rc) return rc;
+    if (!p) return set_error(MIA_ERR_RUNTIME, "decode scratch: null symbol address");
+    addr[dev] = p;
+  }
+  *ptr = addr[dev];
+  return MIA_OK;
+}
 
 DecodePlan plan_decode(const mia_decode_args &a) {
   DecodePlan pl;

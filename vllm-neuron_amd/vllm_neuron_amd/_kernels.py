@@ -247,6 +247,7 @@ def paged_decode(
     split_events: Optional[tuple] = None,
     write_slots: Optional[torch.Tensor] = None,
     k_packed: bool = False,
+    no_alloc: bool = False,
 ) -> torch.Tensor:
     """Attention of ``q [B, S, Hq, d]`` over the paged prior context plus the
     active rows ``k_new/v_new [B, S, Hkv, d]``; returns ``[B, S, Hq, d]`` bf16.
@@ -255,6 +256,10 @@ def paged_decode(
     rows are written to those slots after attention has read the cache;
     slots outside the pool are skipped.  ``k_packed``: ``k_cache`` is the
     packed FP8 layout ``[nb, Hkv, bs/2, d, 2]``, read as it lies.
+    ``no_alloc``: launch through ``mia_paged_decode_noalloc``, whose split-K
+    scratch is the library's static per-device array (``workspace`` is
+    ignored; calls needing more than ``DECODE_NOALLOC_SCRATCH_BYTES`` raise
+    ValueError).
     """
     # every tensor whose address reaches a kernel must live on the device
     dev = N.require_gpu(q, k_new, v_new, k_cache, v_cache, block_table, pos_ids, start_pos,
@@ -367,6 +372,10 @@ def paged_decode(
         a.write_slots = write_slots.data_ptr()
         a.write_slot_dtype = N.mia_dtype(write_slots.dtype)
     L = N.lib()
+    if no_alloc:
+        N.check(L.mia_paged_decode_noalloc(ctypes.byref(a), N.stream_ptr(dev)),
+                "paged_decode (no-alloc)")
+        return out
     need = L.mia_decode_workspace_bytes(ctypes.byref(a))
     if need == 0:
         # argument validation failed; the launch call reports the reason with

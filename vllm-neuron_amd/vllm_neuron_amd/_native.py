@@ -209,8 +209,11 @@ EXPORTS = [
     "mia_paged_decode", "mia_prefill_workspace_bytes", "mia_paged_prefill", "mia_slot_mapping",
     "mia_slot_mapping_host", "mia_remap_null_block", "mia_swa_trim",
     "mia_packed_k_convert", "mia_scatter_rows", "mia_stage_rows", "mia_qkv_epilogue",
-    "mia_row_norm",
+    "mia_row_norm", "mia_paged_decode_noalloc",
 ]
+
+# Static scratch capacity of mia_paged_decode_noalloc (include/mia_attn.h).
+DECODE_NOALLOC_SCRATCH_BYTES = 64 << 20
 
 _lib = None
 _lock = threading.Lock()
@@ -224,6 +227,7 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.mia_args_size.restype = ctypes.c_size_t
     for name, st in (("mia_kv_write", KvWriteArgs), ("mia_gather_kv", GatherArgs),
                      ("mia_decode_mask", MaskArgs), ("mia_paged_decode", DecodeArgs),
+                     ("mia_paged_decode_noalloc", DecodeArgs),
                      ("mia_paged_prefill", PrefillArgs), ("mia_slot_mapping", SlotMappingArgs),
                      ("mia_swa_trim", SwaTrimArgs), ("mia_packed_k_convert", PackedKArgs),
                      ("mia_scatter_rows", ScatterRowsArgs), ("mia_stage_rows", StageArgs),
