@@ -186,3 +186,50 @@ def test_decode_equals_last_prefill_row():
                          vn.view(1, 1, Hkv, d), kc.float(), vc.float(), table,
                          torch.tensor([[float(p)]]), scale=0.125)
     assert (dec[0, 0] - pre[p]).abs().max().item() < 1e-12
+
+
+def test_fp8_per_head_scales_reduce_to_the_scalar_reference_per_kv_head():
+    """Per-(kv head) FP8 scales generalise the reference's scalar [1, 1]
+    scale.  Heads are independent, so running the restated reference decode
+    (attention_decode.py:653-1182) once per kv head h -- cache sliced to h,
+    q heads [hG, (h+1)G), scalar quant scale r_h, 1/r_h folded into the
+    softmax scale and the output as the callers do (llama3/model.py:961-969)
+    -- must give what the float64 oracle gives with the per-head dequant
+    vectors.  A swapped head, an inverted scale or a scale applied to the
+    wrong operand fails this."""
+    B, S, Hq, Hkv, d, bs, nblk, nb = 3, 1, 8, 2, 64, 16, 8, 40
+    G = Hq // Hkv
+    q, kn, vn, kc, vc, table, pos = _decode_inputs(B, S, Hq, Hkv, d, bs, nblk, seed=9, nb=nb)
+    f8 = torch.float8_e4m3fn
+    # quant scales as the reference loads them (bf16 reciprocals), dequant = 1 / quant
+    r_k = torch.tensor([55.0, 14.0]).to(torch.bfloat16)
+    r_v = torch.tensor([20.0, 90.0]).to(torch.bfloat16)
+    s_k, s_v = 1.0 / r_k.double(), 1.0 / r_v.double()
+
+    def quant(x, r):
+        return (x * r).clamp(-448.0, 448.0).to(f8)
+
+    kc8 = torch.stack([quant(kc[:, h], r_k[h]) for h in range(Hkv)], 1)
+    vc8 = torch.stack([quant(vc[:, h], r_v[h]) for h in range(Hkv)], 1)
+    scale = d ** -0.5
+    rts = {"k": r_k, "v": r_v}
+    full = OD.fp32_decode(q, kn, vn, kc8.double(), vc8.double(), table, pos, scale=scale,
+                          k_deq=s_k, v_deq=s_v,
+                          fp8_roundtrip=lambda x, h, kind: quant(x, rts[kind][h]).double())
+    for h in range(Hkv):
+        X = torch.cat([q[:, :, h * G:(h + 1) * G].reshape(B, S, -1), kn[:, :, h], vn[:, :, h]],
+                      -1)
+        W = torch.eye(X.shape[-1], dtype=torch.bfloat16)
+        mask = OM.gen_mask_torch(pos.reshape(1, -1), B, G, S, nblk * bs, block_len=bs)
+        out = OD.ref_attention_decode(
+            X, W, kc8[:, h:h + 1].clone(), vc8[:, h:h + 1].clone(), table, mask,
+            softmax_scale=scale * float(s_k[h]), k_scale=r_k[h].view(1, 1),
+            v_scale=r_v[h].view(1, 1))[0]                       # [B, G, d, S]
+        got = out.double().permute(0, 3, 1, 2) * float(s_v[h])  # [B, S, G, d]
+        err = (got - full[:, :, h * G:(h + 1) * G]).abs().max().item()
+        assert err <= TOL, f"kv head {h}: {err}"
+    # and the per-head result is not what one shared scale would give
+    wrong = OD.fp32_decode(q, kn, vn, kc8.double(), vc8.double(), table, pos, scale=scale,
+                           k_deq=s_k.flip(0), v_deq=s_v.flip(0),
+                           fp8_roundtrip=lambda x, h, kind: quant(x, rts[kind][h]).double())
+    assert (wrong - full).abs().max().item() > 10 * TOL

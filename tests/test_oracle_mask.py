@@ -7,7 +7,9 @@ Pins oracle/mask.py (torch restatement of attention_decode_mask.py) with:
   ``j < min(pos)``, sliding window ``start <= j < min(pos)`` and its wrap
   case, the triu overlay on the last S_tkg slots;
 * the C restatement (bit-exact, including the ValueError / IndexError cases);
-* the product's host helpers (block-length resize, index maps).
+* the product's host helpers (block-length resize, index maps);
+* the block-length resize by known answers worked from the reference's
+  stated sharding rules.
 """
 import numpy as np
 import pytest
@@ -52,6 +54,53 @@ def test_resize_block_len(bl, bs, qh, sa, sp):
     assert r == C.resize_block_len(bl, bs, qh, sa, sp) == PM._resize_block_len(bl, bs, qh, sa, sp)
     if bl > 0 and r != bl:
         assert bl % r == 0 and (sp // 128) % r == 0
+
+
+# Known answers worked by hand from the rules stated in the reference's
+# docstring and NOTE (attention_decode_mask.py:294-303), not from its code:
+#   batch sharded  <=> bs even and (bs*q_head*s_active >= 128 or s_prior <= 256)
+#   s_prior sharded <=> not batch sharded and s_prior >= 256  (n_prgs 2, else 1)
+#   bucket = (s_prior // bl) * bl; if bucket % (n_prgs * 128): bl unchanged,
+#   else gcd(bl, bucket / (n_prgs * 128)).
+# Each row names the slip it catches.
+@pytest.mark.parametrize("bl,bs,qh,sa,sp,want", [
+    # odd bs: never batch sharded, so s_prior 256 shards (n=2): gcd(32, 256/256) = 1;
+    # the precedence slip "(even and A) or s_prior <= 256" gives n=1 -> 2
+    (32, 1, 32, 1, 256, 1),
+    # even bs, product 64 < 128, s_prior exactly 256: batch sharded by the <= 256
+    # threshold (n=1) -> gcd(32, 2) = 2; "< 256" would give n=2 -> 1
+    (32, 2, 32, 1, 256, 2),
+    # s_prior 384 > 256 with product 64: s_prior sharded (n=2); 384 % 256 != 0 -> 32 kept
+    (32, 2, 32, 1, 384, 32),
+    # product 128 >= 128 (even bs): batch sharded, n=1; 384 % 128 == 0 -> gcd(32, 3) = 1
+    (32, 2, 64, 1, 384, 1),
+    # product 126 < 128 at s_prior 512: s_prior sharded -> gcd(32, 512/256) = 2
+    (32, 2, 63, 1, 512, 2),
+    # product 128 at s_prior 512: batch sharded -> gcd(32, 512/128) = 4
+    (32, 2, 64, 1, 512, 4),
+    # odd bs ignores the product: 127 and 128 heads both s_prior sharded -> 2
+    (32, 1, 127, 1, 512, 2),
+    (32, 1, 128, 1, 512, 2),
+    # s_active enters the product: 2 * 32 * 2 = 128 -> batch sharded -> 4
+    (32, 2, 32, 2, 512, 4),
+    # s_prior 128 < 256, odd bs: n=1 -> gcd(32, 1) = 1
+    (32, 1, 8, 1, 128, 1),
+    # block_len 48 (not a power of two): n=1 -> gcd(48, 384/128 = 3) = 3;
+    # with odd bs n=2 and 384 % 256 != 0 -> 48 kept
+    (48, 2, 64, 1, 384, 3),
+    (48, 1, 64, 1, 384, 48),
+    # s_prior not a multiple of block_len: bucket 500 % 256 != 0 -> 100 kept
+    (100, 1, 8, 1, 512, 100),
+    # the Llama-3-8B decode mask (bs 64, 32 heads, 8192 tokens, bl 32):
+    # batch sharded -> gcd(32, 8192/128 = 64) = 32 (unchanged)
+    (32, 64, 32, 1, 8192, 32),
+    # block_len 0 (no block KV) passes through
+    (0, 4, 4, 1, 512, 0),
+])
+def test_resize_block_len_known_answers(bl, bs, qh, sa, sp, want):
+    assert OM.resize_block_len(bl, bs, qh, sa, sp) == want
+    assert PM._resize_block_len(bl, bs, qh, sa, sp) == want
+    assert C.resize_block_len(bl, bs, qh, sa, sp) == want
 
 
 def _unpermuted(mask, bl, B, Hq, S, sp):

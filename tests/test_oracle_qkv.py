@@ -159,3 +159,39 @@ def test_cache_write_rule(fp8):
             assert torch.equal(vc[blk, :, off].view(torch.uint8), vr.view(torch.uint8))
     u8 = lambda c: c.view(torch.uint8).permute(0, 2, 1, 3)[~written]   # untouched slots
     assert torch.equal(u8(kc), u8(kc0)) and torch.equal(u8(vc), u8(vc0))
+
+
+@pytest.mark.parametrize("contiguous", [True, False])
+def test_decode_rope_is_the_pairwise_rotation(contiguous):
+    """The decode RoPE restatement (attention_decode.py:470-509) against an
+    element loop of the rotation itself, in float64: pair (a, b) of channel
+    pair i -- (x[i], x[i + d/2]) half-split, (x[2i], x[2i+1]) interleaved --
+    becomes (a cos_i - b sin_i, b cos_i + a sin_i) with cos/sin [d/2, B, S].
+    A flipped sign, swapped halves or a wrong pairing fails here (comparing
+    the two layouts with each other would not catch an error they share)."""
+    B, S, Hq, Hkv, d = 2, 3, 3, 2, 8
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(B, Hq, S, d, generator=g, dtype=torch.float64)
+    k = torch.randn(B, Hkv, S, d, generator=g, dtype=torch.float64)
+    ang = torch.rand(d // 2, B, S, generator=g, dtype=torch.float64) * 6.0
+    cos, sin = torch.cos(ang), torch.sin(ang)
+    qr, kr = OQ._rope_decode(q, k, cos, sin, contiguous)
+
+    def rotate(x):
+        y = torch.empty_like(x)
+        for b in range(x.shape[0]):
+            for h in range(x.shape[1]):
+                for s in range(S):
+                    for i in range(d // 2):
+                        ia, ib = (i, i + d // 2) if contiguous else (2 * i, 2 * i + 1)
+                        a, bb = float(x[b, h, s, ia]), float(x[b, h, s, ib])
+                        c, sn = float(cos[i, b, s]), float(sin[i, b, s])
+                        y[b, h, s, ia] = a * c - bb * sn
+                        y[b, h, s, ib] = bb * c + a * sn
+        return y
+
+    assert (qr - rotate(q)).abs().max().item() < 1e-12
+    assert (kr - rotate(k)).abs().max().item() < 1e-12
+    # rotation by the angle's negative undoes it
+    q2, _ = OQ._rope_decode(qr, kr, cos, -sin, contiguous)
+    assert (q2 - q).abs().max().item() < 1e-12

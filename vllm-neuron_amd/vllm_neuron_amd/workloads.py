@@ -274,6 +274,37 @@ def make_prefill_batch(cfg: PrefillConfig, device="cpu") -> PrefillBatch:
                         prior.to(torch.int32).to(dev), slots.to(dev), S, kd, vd, kq, vq)
 
 
+@dataclass
+class MixedBatch:
+    """Decode rows and prefill sequences over one shared cache pool: the
+    decode batch's blocks follow the prefill batch's (tables and slots
+    shifted accordingly), block 0 stays the null block."""
+    decode: DecodeBatch
+    prefill: PrefillBatch
+    k_cache: torch.Tensor
+    v_cache: torch.Tensor
+
+
+def make_mixed_batch(device="cpu",
+                     decode_cfg: Optional[DecodeConfig] = None,
+                     prefill_cfg: Optional[PrefillConfig] = None) -> MixedBatch:
+    """The Llama-3-8B mixed chunked-prefill batch by default: 4 x 512 new
+    tokens on priors U[0, 4096] plus 60 decode rows at contexts U[1k, 8k]."""
+    dcfg = decode_cfg or DECODE_CONFIGS["llama3_8b_mixed_decode_b60"]
+    pcfg = prefill_cfg or PREFILL_CONFIGS["llama3_8b_prefill_4x512"]
+    pb = make_prefill_batch(pcfg, device)
+    db = make_decode_batch(dcfg, device)
+    nb_p = pb.k_cache.shape[0]
+    k_cache = torch.cat([pb.k_cache, db.k_cache[1:]], 0)
+    v_cache = torch.cat([pb.v_cache, db.v_cache[1:]], 0)
+    pb.k_cache, pb.v_cache = k_cache, v_cache
+    shift = nb_p - 1
+    db.block_table = torch.where(db.block_table > 0, db.block_table + shift, db.block_table)
+    db.slots = db.slots + shift * dcfg.block_size
+    db.k_cache, db.v_cache = k_cache, v_cache
+    return MixedBatch(db, pb, k_cache, v_cache)
+
+
 # ---------------------------------------------------------------------------
 # algorithmic work
 # ---------------------------------------------------------------------------
