@@ -34,7 +34,7 @@ from typing import Optional, Tuple, Union
 import torch
 from torch import Tensor
 
-from ... import _kernels as K
+from ... import ops as K
 
 _TILE = 64  # keys per kernel tile (the padded key buffer is a whole number of tiles)
 

@@ -37,7 +37,7 @@ from typing import Optional, Tuple
 import torch
 from torch import Tensor
 
-from ... import _kernels as K
+from ... import ops as K
 from ... import _native as N
 from ...utils.common_types import QuantizationType
 from .attention_decode_mask import (

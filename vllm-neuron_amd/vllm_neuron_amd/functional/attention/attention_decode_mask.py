@@ -21,7 +21,7 @@ from typing import Optional
 import torch
 from torch import Tensor
 
-from ... import _kernels as K
+from ... import ops as K
 
 P_MAX = 128
 
@@ -145,6 +145,10 @@ def gen_attention_decode_mask(
             raise IndexError(
                 f"index {lin} is out of bounds for dimension 0 with size {s_prior}")
     mask = K.decode_mask(pos_ids, bs, q_head, s_active, s_prior, start_pos, bl)
+    if torch.compiler.is_compiling():
+        # a Python attribute does not survive tracing: the compiled decode
+        # reads this mask as given (the full-mask path)
+        return mask
     # The descriptor keeps its own copy of the positions (B*S floats): the
     # mask encodes the positions as they are now, and a caller that later
     # updates its position buffer in place must not change what the kernel
@@ -159,6 +163,8 @@ def gen_attention_decode_mask(
 def mask_descriptor(mask: Optional[Tensor]) -> Optional[_MaskDesc]:
     """The generating positions of an unmodified mask from
     :func:`gen_attention_decode_mask`, else None."""
+    if mask is None or torch.compiler.is_compiling():
+        return None
     desc = getattr(mask, "_mia_desc", None)
     if desc is None or mask._version != desc.version:
         return None

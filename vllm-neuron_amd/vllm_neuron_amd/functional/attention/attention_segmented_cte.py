@@ -25,7 +25,7 @@ from typing import Optional
 import torch
 from torch import Tensor
 
-from ... import _kernels as K
+from ... import ops as K
 from .attention_decode import _unswizzle_packed_k
 
 _MAX_HEAD_DIM = 128

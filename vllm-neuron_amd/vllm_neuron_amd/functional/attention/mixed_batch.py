@@ -20,7 +20,7 @@ from typing import Optional, Tuple
 import torch
 from torch import Tensor
 
-from ... import _kernels as K
+from ... import ops as K
 from .attention_decode import _quant_mode_for, _scale_per_head, paged_decode_core
 
 

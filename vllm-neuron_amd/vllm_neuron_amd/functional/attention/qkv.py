@@ -33,7 +33,7 @@ from typing import Optional
 import torch
 from torch import Tensor
 
-from ... import _kernels as K
+from ... import ops as K
 from ... import _native as N
 from ...utils.common_types import NormType, QKVOutputLayout, QKVWeightLayout, QuantizationType
 

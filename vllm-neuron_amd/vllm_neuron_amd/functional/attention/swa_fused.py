@@ -34,7 +34,7 @@ from typing import Optional, Tuple
 import torch
 from torch import Tensor
 
-from ... import _kernels as K
+from ... import ops as K
 from ... import _native as N
 from .attention_cte import flash_attention
 

@@ -16,7 +16,7 @@ from typing import Optional
 import numpy as np
 import torch
 
-from ... import _kernels as K
+from ... import ops as K
 from ... import _native as N
 
 NULL_BLOCK_ID = 0
