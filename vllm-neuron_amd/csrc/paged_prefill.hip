@@ -46,6 +46,8 @@ constexpr int kRowsW = 32;    // query rows per wave
 constexpr int kKT = 64;       // keys per tile
 constexpr int kKPad = 8;      // bf16 padding per K row in LDS
 constexpr int kVPad = 8;      // bf16 padding per V^T row in LDS
+constexpr int kPartPad = 4;   // a split partial row: o[D], m, l and 2 floats of padding
+constexpr int kMaxChunks = 8; // key chunks of a split row tile at most
 
 struct PrefillKParams {
   const uint16_t *q;
@@ -71,7 +73,7 @@ struct PrefillKParams {
   uint16_t *out;
   int64_t os_t, os_h;
   // split-K over keys (nsplit == 1: off)
-  float *ws;      // [num_seqs, Hkv, rows_max, nsplit, D + 2] fp32 partials
+  float *ws;      // [num_seqs, Hkv, rows_max, nsplit, D + 4] fp32 partials (o, m, l, pad)
   int nsplit;     // chunks per row tile at most (grid z = nsplit * num_seqs)
   int num_seqs;
   int ksplit;     // keys per chunk (multiple of the 64-key tile)
@@ -85,6 +87,7 @@ struct PrefillKParams {
   int non_causal;                 // every existing key visible
   int q_off;                      // added to query positions
   int uniform;                    // empty rows (no sink) attend uniformly
+  int rank_items;                 // order work items by cost (several sequences)
 };
 
 // Key range of the workgroup whose rows start at row0 (rows are GQA-packed:
@@ -212,6 +215,91 @@ MIA_DEV int split_keys(const PrefillKParams &p) {
   return p.nsplit <= 1 ? (1 << 30) : p.ksplit;
 }
 
+// Key tiles (plus one for the fixed per-workgroup cost) of work item
+// (row tile rt, group g = kv head + Hkv * (chunk * num_seqs + sequence));
+// 0 for an item that exits at once (rows past the sequence, or a chunk past
+// the row tile's key range).  The kv head does not change the cost.
+MIA_DEV int item_cost(const PrefillKParams &p, int rt, int g) {
+  const int z = g / p.Hkv;
+  const int sp = z / p.num_seqs;
+  const int seq = z - sp * p.num_seqs;
+  const int q_begin = p.cu[seq];
+  const int S_q = p.cu[seq + 1] - q_begin;
+  const int row0 = rt * p.rows_wg;
+  if (row0 >= S_q * p.G) return 0;
+  const int ksplit = split_keys(p);
+  const KeyRange kr = wg_key_range(p, seq, p.prior[seq], S_q, row0, ksplit);
+  if (sp >= kr.n_sp) return 0;
+  if (!kr.any) return 1;
+  int kt0 = kr.kt0, kt_last = kr.kt_last;
+  if (kr.n_sp > 1) {
+    const int c = kt0 / ksplit + sp;
+    kt0 = max(kt0, c * ksplit);
+    kt_last = min(kt_last, c * ksplit + ksplit - kKT);
+  }
+  return (kt_last - kt0) / kKT + 2;
+}
+
+constexpr uint32_t kRankMax = 512;  // items per XCD ranked at most
+
+// Work item of this workgroup, heaviest first.  Workgroups are dispatched
+// to the 8 XCDs round-robin by linear id and, within an XCD, in order as
+// earlier ones finish.  All items of a group (kv head, chunk, sequence) stay
+// on one XCD as in xcd_tile (they read the same K/V tiles from its L2), and
+// the k-th workgroup dispatched on an XCD takes that XCD's item of rank k by
+// cost (key tiles; ties keep the launch order), so the in-order dispatch is
+// a longest-first list schedule.  It pays when sequences differ in length:
+// on the Llama-3-8B 4 x 512 chunked prefill (priors 3584, 416, 544, 32) the
+// simulated makespan drops from 32 to 24 key tiles per CU (22.75 ideal) and
+// the launch from ~88 to ~81 us; ranking costs each workgroup a few us at
+// its start (the cost inputs are global loads), so it is used for batches
+// of several sequences only.  For one sequence the row tiles already go
+// heaviest first (xcd_tile).
+// Every thread of the workgroup must call this (two barriers); `scratch`
+// holds cap ints of 16-byte aligned LDS.  Falls back to xcd_tile when the
+// host did not ask for ranking, the group count is not a multiple of 8 or
+// an XCD has more items than the scratch or kRankMax.
+MIA_DEV uint3 ranked_tile(const PrefillKParams &p, int *scratch, int cap) {
+  constexpr uint32_t X = 8;
+  const uint32_t R = gridDim.x;
+  const uint32_t groups = gridDim.y * gridDim.z;
+  const uint32_t n_x = R * (groups / X);  // items per XCD
+  const uint32_t n4 = (n_x + 3) & ~3u;     // costs padded to 16-byte groups
+  if (!p.rank_items || groups % X != 0 || n4 + 1 > (uint32_t)cap || n_x > kRankMax)
+    return xcd_tile();
+  const uint32_t L = blockIdx.x + R * (blockIdx.y + gridDim.y * blockIdx.z);
+  const uint32_t x = L % X, k = L / X;
+  // item j of XCD x: row tile j % R of group x + 8 (j / R); padding costs -1
+  // rank nothing (real costs are >= 0)
+  for (uint32_t j = threadIdx.x; j < n4; j += blockDim.x)
+    scratch[j] = j < n_x ? item_cost(p, (int)(j % R), (int)(x + X * (j / R))) : -1;
+  __syncthreads();
+  // rank of item j: items of higher cost, or of equal cost and lower index.
+  // Costs are read 4 per 16-byte LDS load, 4 loads in flight.
+  typedef int i32x4_t __attribute__((ext_vector_type(4)));
+  const i32x4_t *c4 = reinterpret_cast<const i32x4_t *>(scratch);
+  for (uint32_t j = threadIdx.x; j < n_x; j += blockDim.x) {
+    const int c = scratch[j];
+    uint32_t rank = 0;
+#pragma unroll 4
+    for (uint32_t i4 = 0; i4 < n4 / 4; ++i4) {
+      const i32x4_t ci = c4[i4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        rank += (ci[e] > c) || (ci[e] == c && 4 * i4 + e < j);
+    }
+    if (rank == k) scratch[n4] = (int)j;
+  }
+  __syncthreads();
+  const uint32_t j = (uint32_t)scratch[n4];
+  const uint32_t g = x + X * (j / R);
+  uint3 t;
+  t.x = j % R;
+  t.y = g % gridDim.y;
+  t.z = g / gridDim.y;
+  return t;
+}
+
 // Epilogue shared by the attention kernels.  Lane holds O^T[d][row] for
 // d = db*32 + (e/4)*8 + half*4 + e%4 of its row (lane % 32); m_run / l_run
 // are the row's running max (log2 domain) and this lane's partial sum.
@@ -258,7 +346,7 @@ MIA_DEV void finish_rows(const PrefillKParams &p, const f32x16_t (&acc_o)[D / 32
     // prefill_combine_kernel
     if (row_ok) {
       float *w = p.ws + ((((int64_t)seq * p.Hkv + h) * p.rows_max + r) * p.nsplit + sp) *
-                            (int64_t)(D + 2);
+                            (int64_t)(D + kPartPad);
 #pragma unroll
       for (int db = 0; db < D / 32; ++db)
 #pragma unroll
@@ -268,10 +356,7 @@ MIA_DEV void finish_rows(const PrefillKParams &p, const f32x16_t (&acc_o)[D / 32
               f32x4_t{acc_o[db][e4 * 4] * vscale, acc_o[db][e4 * 4 + 1] * vscale,
                       acc_o[db][e4 * 4 + 2] * vscale, acc_o[db][e4 * 4 + 3] * vscale};
         }
-      if (half == 0) {
-        w[D] = m_run;
-        w[D + 1] = l_run;
-      }
+      if (half == 0) *reinterpret_cast<float2 *>(w + D) = make_float2(m_run, l_run);
     }
     return;
   }
@@ -316,9 +401,10 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[kKT * KROW];
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[D * VROW];
 
-  // chunk-major grid: the workgroups of high chunk indices, which exit at
-  // once for row tiles with fewer chunks, are dispatched last
-  const uint3 tile = xcd_tile();
+  // heaviest work item first (the K tile buffer is free until the loop)
+  const uint3 tile = ranked_tile(p, reinterpret_cast<int *>(k_lds),
+                                 (int)(sizeof(k_lds) / sizeof(int)));
+  __syncthreads();  // the ranking scratch is read before the first K tile store
   const int sp = tile.z / p.num_seqs;  // key chunk of a split row tile
   const int seq = tile.z - sp * p.num_seqs;
   const int h = tile.y;
@@ -604,16 +690,16 @@ __global__ __launch_bounds__(512, 1) void prefill_dma_kernel(PrefillKParams p) {
   typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
   typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
 
-  __shared__ int32_t ids_lds[kDmaIds];
+  __shared__ __attribute__((aligned(16))) int32_t ids_lds[kDmaIds];
   __shared__ __attribute__((aligned(1024))) uint8_t kv_lds[3][2][TILEB];  // [stage][K, V]
   // LDS addresses are handled as LDS pointers / integers only: a generic
   // pointer to shared memory carried through the loops would need the
   // aperture conversion at every use
   lds_u8_t *const kv_base = (lds_u8_t *)&kv_lds[0][0][0];
 
-  // chunk-major grid: the workgroups of high chunk indices, which exit at
-  // once for row tiles with fewer chunks, are dispatched last
-  const uint3 tile = xcd_tile();
+  // heaviest work item first (the block-id buffer is free until it is filled)
+  const uint3 tile = ranked_tile(p, ids_lds, kDmaIds);
+  __syncthreads();  // the ranking scratch is read before the block ids land
   const int sp = tile.z / p.num_seqs;  // key chunk of a split row tile
   const int seq = tile.z - sp * p.num_seqs;
   const int h = tile.y;
@@ -870,86 +956,74 @@ __global__ __launch_bounds__(512, 1) void prefill_dma_kernel(PrefillKParams p) {
 // ---------------------------------------------------------------------------
 // split-K merge
 // ---------------------------------------------------------------------------
-// One wave per query row (4 rows per workgroup); rows of tiles that were
-// not split exit at once.  The n_sp partials (o, m, l) of the row (log2
-// domain) are loaded together, the sink joins the denominator, and the
-// bf16 row is written.
-// Merge of the split rows: 16 rows per workgroup (grid over all rows;
-// rows of unsplit tiles exit at once); each wave loads the n_sp partials
-// (o, m, l) of its 4 rows together (log2 domain), adds the sink to the
-// denominator and writes the bf16 rows.
+// 64 rows per workgroup (rows of unsplit row tiles exit at once).  A row's
+// partial of one chunk is D fp32 (16-byte aligned rows of D + 4 floats), so
+// D/4 lanes cover it with one 16-byte load each and a wave steps over
+// 64/(D/4) rows at a time; all chunks' loads of a step are issued together.
+// The n_sp partials (o, m, l; log2 domain) are merged in chunk order, the
+// sink joins the denominator and the bf16 row is stored (8 bytes per lane).
 template <int D>
 __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillKParams p) {
-  constexpr int DPL = D / 64;  // d values per lane
-  constexpr int kMaxSp = 8;
-  constexpr int RPW = 4;       // rows per wave, loaded together
+  constexpr int kRows = 64;          // rows per workgroup (4 waves x 16)
+  constexpr int LPR = D / 4;         // lanes per row
+  constexpr int RPS = 64 / LPR;      // rows per wave step
+  constexpr int kSteps = 16 / RPS;
+  constexpr int PS = D + kPartPad;   // floats per partial row
   const int seq = blockIdx.z;
   const int h = blockIdx.y;
   const int q_begin = p.cu[seq];
   const int S_q = p.cu[seq + 1] - q_begin;
   const int rows_total = S_q * p.G;
-  const int r0 = blockIdx.x * 16;  // inside one row tile (rows_wg % 16 == 0)
-  if (r0 >= rows_total) return;
+  const int row0 = blockIdx.x * kRows;  // inside one row tile (rows_wg % 64 == 0)
+  if (row0 >= rows_total) return;
   const KeyRange kr =
-      wg_key_range(p, seq, p.prior[seq], S_q, (r0 / p.rows_wg) * p.rows_wg, split_keys(p));
+      wg_key_range(p, seq, p.prior[seq], S_q, (row0 / p.rows_wg) * p.rows_wg, split_keys(p));
   if (kr.n_sp <= 1) return;
-  const int n_sp = min(kr.n_sp, kMaxSp);
+  const int n_sp = min(kr.n_sp, kMaxChunks);
+  const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
-  const int rw = r0 + (threadIdx.x >> 6) * RPW;
-  if (rw >= rows_total) return;
-  float m[RPW][kMaxSp], l[RPW][kMaxSp], o[RPW][kMaxSp][DPL];
+  const int sub = lane / LPR;
+  const int c4 = (lane % LPR) * 4;
+  const int64_t base = ((int64_t)seq * p.Hkv + h) * p.rows_max;
+#pragma unroll 2
+  for (int step = 0; step < kSteps; ++step) {
+    const int r = row0 + wave * 16 + step * RPS + sub;
+    const bool ok = r < rows_total;
+    const int rc = ok ? r : rows_total - 1;  // loads stay inside written rows
+    const float *w0 = p.ws + (base + rc) * p.nsplit * (int64_t)PS;
+    f32x4_t o[kMaxChunks];
+    float2 ml[kMaxChunks];
 #pragma unroll
-  for (int i = 0; i < RPW; ++i) {
-    const int r = min(rw + i, rows_total - 1);
-    const float *w0 =
-        p.ws + (((int64_t)seq * p.Hkv + h) * p.rows_max + r) * p.nsplit * (int64_t)(D + 2);
-#pragma unroll
-    for (int j = 0; j < kMaxSp; ++j) {
-      m[i][j] = -INFINITY;
-      l[i][j] = 0.f;
-#pragma unroll
-      for (int e = 0; e < DPL; ++e) o[i][j][e] = 0.f;
-      if (j < n_sp) {  // only the chunks that exist (uniform)
-        const float *w = w0 + j * (D + 2);
-        m[i][j] = w[D];
-        l[i][j] = w[D + 1];
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) o[i][j][e] = w[lane * DPL + e];
+    for (int j = 0; j < kMaxChunks; ++j) {
+      if (j < n_sp) {
+        o[j] = *reinterpret_cast<const f32x4_t *>(w0 + j * PS + c4);
+        ml[j] = *reinterpret_cast<const float2 *>(w0 + j * PS + D);
       }
     }
-  }
-#pragma unroll
-  for (int i = 0; i < RPW; ++i) {
-    const int r = rw + i;
-    if (r >= rows_total) break;
-    const int pos_r = r / p.G;
-    const int hq = h * p.G + (r - pos_r * p.G);
-    if (q_begin + pos_r >= p.num_tokens) continue;
+    const int pos_r = rc / p.G;
+    const int hq = h * p.G + (rc - pos_r * p.G);
     const float sink2 = p.sink ? p.sink[hq] * kLog2e : -INFINITY;
     float M = sink2;
 #pragma unroll
-    for (int j = 0; j < kMaxSp; ++j)
-      if (j < n_sp) M = fmaxf(M, m[i][j]);
+    for (int j = 0; j < kMaxChunks; ++j)
+      if (j < n_sp) M = fmaxf(M, ml[j].x);
     const float Mu = (M == -INFINITY) ? 0.f : M;
     float L = __builtin_amdgcn_exp2f(sink2 - Mu);
-    float acc[DPL];
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int e = 0; e < DPL; ++e) acc[e] = 0.f;
-#pragma unroll
-    for (int j = 0; j < kMaxSp; ++j) {
+    for (int j = 0; j < kMaxChunks; ++j) {
       if (j < n_sp) {
-        const float f = __builtin_amdgcn_exp2f(m[i][j] - Mu);
-        L += l[i][j] * f;
+        const float f = __builtin_amdgcn_exp2f(ml[j].x - Mu);
+        L += ml[j].y * f;
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) acc[e] += o[i][j][e] * f;
+        for (int e = 0; e < 4; ++e) acc[e] += o[j][e] * f;
       }
     }
     const float inv = L > 0.f ? 1.0f / L : 0.f;
-    uint16_t *op = p.out + (int64_t)(q_begin + pos_r) * p.os_t + (int64_t)hq * p.os_h;
-    if constexpr (DPL == 2) {
-      *reinterpret_cast<uint32_t *>(op + lane * 2) = pack2_bf16(acc[0] * inv, acc[1] * inv);
-    } else {
-      op[lane] = (uint16_t)f32_to_bf16_bits(acc[0] * inv);
+    if (ok && q_begin + pos_r < p.num_tokens) {
+      uint16_t *op = p.out + (int64_t)(q_begin + pos_r) * p.os_t + (int64_t)hq * p.os_h + c4;
+      *reinterpret_cast<u32x2_t *>(op) =
+          u32x2_t{pack2_bf16(acc[0] * inv, acc[1] * inv), pack2_bf16(acc[2] * inv, acc[3] * inv)};
     }
   }
 }
@@ -1011,7 +1085,7 @@ PrefillPlan plan_prefill(const mia_prefill_args &a) {
              ? std::max<int64_t>(1024, ((s_ctx + 2) / 3 + 511) / 512 * 512)
              : (int64_t)1 << 30;
   }
-  ks = std::max<int64_t>(ks, (s_ctx + 7) / 8);  // the merge holds 8 partials
+  ks = std::max<int64_t>(ks, (s_ctx + kMaxChunks - 1) / kMaxChunks);  // merged in registers
   ks = std::max<int64_t>(kKT, ((ks + kKT - 1) / kKT) * kKT);
   pl.ksplit = (int)std::min<int64_t>(ks, 1 << 30);
   pl.nsplit = s_ctx > 0 ? (int)((s_ctx + pl.ksplit - 1) / pl.ksplit) : 1;
@@ -1020,7 +1094,7 @@ PrefillPlan plan_prefill(const mia_prefill_args &a) {
     pl.ws_bytes = 0;
   } else {
     pl.ws_bytes = (size_t)a.num_seqs * a.num_kv_heads * pl.rows_max * pl.nsplit *
-                                   (a.head_dim + 2) * sizeof(float);
+                                   (a.head_dim + kPartPad) * sizeof(float);
   }
   return pl;
 }
@@ -1079,6 +1153,7 @@ int launch_paged_prefill(const mia_prefill_args &a, const PrefillPlan &pl, hipSt
   kp.non_causal = a.non_causal ? 1 : 0;
   kp.q_off = a.q_offset;
   kp.uniform = a.empty_rows_uniform ? 1 : 0;
+  kp.rank_items = a.num_seqs > 1 ? 1 : 0;
   const dim3 grid((unsigned)((pl.rows_max + pl.rows_wg - 1) / pl.rows_wg),
                   (unsigned)a.num_kv_heads, (unsigned)(pl.nsplit * a.num_seqs));
   if (pl.dma) {
@@ -1094,7 +1169,7 @@ int launch_paged_prefill(const mia_prefill_args &a, const PrefillPlan &pl, hipSt
   }
   int rc = check_hip(hipGetLastError(), "prefill launch");
   if (rc || pl.nsplit <= 1) return rc;
-  const dim3 cgrid((unsigned)((pl.rows_max + 15) / 16), (unsigned)a.num_kv_heads,
+  const dim3 cgrid((unsigned)((pl.rows_max + 63) / 64), (unsigned)a.num_kv_heads,
                    (unsigned)a.num_seqs);
   if (a.head_dim == 128)
     hipLaunchKernelGGL((prefill_combine_kernel<128>), cgrid, dim3(256), 0, s, kp);
