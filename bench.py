@@ -16,6 +16,10 @@ The same line carries
   * ``prefill``: the chunked-prefill sub-batch of the mixed Llama-3-8B
     workload (4 sequences x 512 new tokens on priors U[0, 4096]) in TFLOP/s
     against the bf16 MFMA peak;
+  * ``secondary``: the other workloads (GPT-OSS-120B-shaped decode layers,
+    long-context FP8 decode, Llama-3.2-1B decode, 2048-token FP8 prefill
+    chunk, Llama-3-8B mixed batch) in µs per call from HIP graph replays,
+    each with its algorithmic rate and roofline fraction;
   * ``cpu_baseline``: the CPU restatement of the reference's torch decode
     path on a bounded sample of the same workload, timed on this host.
 """
@@ -139,6 +143,137 @@ def bench_prefill(dev, steps, warmup):
     return dict(flops=flops, ms=ms, ms_med=ms, tflops=flops / (ms * 1e-3) / 1e12)
 
 
+def _graph_us(fn, dev, reps: int, per_graph: int = 8) -> float:
+    """GPU time of one ``fn()`` call: ``per_graph`` calls captured in one HIP
+    graph, replayed ``reps`` times between one event pair (no per-call host
+    launch cost in the timed region; the graph launch is amortised over
+    ``per_graph`` calls)."""
+    import torch
+
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):
+        fn()  # warm-up (allocator, library load) outside the capture
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(per_graph):
+            fn()
+    for _ in range(2):
+        graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        graph.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
+
+
+def bench_secondary(dev, reps: int) -> dict:
+    """The other benchmark workloads, each as µs per call (HIP graph replay)
+    with its algorithmic rate and roofline fraction: GPT-OSS-120B-shaped
+    decode (full-attention and 128-token sliding-window layers, sinks), the
+    long-context FP8 decode, the Llama-3.2-1B decode, the 2048-token FP8
+    prefill chunk, and the Llama-3-8B mixed batch (4 x 512 chunked prefill +
+    60 decode rows) as one call against max(bytes / HBM peak, FLOPs / bf16
+    peak)."""
+    import torch
+
+    from vllm_neuron_amd import _kernels as K
+    from vllm_neuron_amd import _native as N
+    from vllm_neuron_amd import workloads as W
+    from vllm_neuron_amd.functional import mixed_batch_attention
+    from vllm_neuron_amd.functional.attention.attention_decode import paged_decode_core
+
+    out = {}
+    for name in ("gptoss_decode_full_b32", "gptoss_decode_swa_b32", "fp8_decode_b16_32k",
+                 "llama3_1b_decode_b4"):
+        cfg = W.DECODE_CONFIGS[name]
+        b = W.make_decode_batch(cfg, dev)
+        S_ctx = b.block_table.shape[1] * cfg.block_size
+        ws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+        slots = b.slots.reshape(-1).contiguous()
+        kw = {}
+        if cfg.fp8:
+            kw = dict(k_scale=b.k_quant, v_scale=b.v_quant, k_dequant_scale=b.k_dequant,
+                      v_dequant_scale=b.v_dequant)
+
+        def step(b=b, S_ctx=S_ctx, ws=ws, slots=slots, kw=kw, cfg=cfg):
+            paged_decode_core(b.q, b.k_new, b.v_new, b.k_cache, b.v_cache, b.block_table,
+                              block_len=cfg.block_size, S_ctx=S_ctx, pos_ids=b.pos,
+                              swa_start_pos_ids=b.start, sink=b.sink,
+                              softmax_scale=cfg.head_dim ** -0.5, workspace=ws,
+                              write_slots=slots, **kw)
+
+        us = _graph_us(step, dev, reps)
+        nbytes = W.decode_bytes(b)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        rec = {"us_per_call": round(us, 2), "algorithmic_bytes": nbytes, "GB_s": round(gbs, 1)}
+        if nbytes > 256 << 20:  # HBM-bound (beyond the 256 MB memory-side cache)
+            rec.update(bound="hbm", frac=round(gbs / HBM_PEAK_GBS, 4))
+        else:
+            rec.update(bound="latency")
+        out[name] = rec
+        del b, ws
+    for name in ("fp8_prefill_2048",):
+        cfg = W.PREFILL_CONFIGS[name]
+        b = W.make_prefill_batch(cfg, dev)
+        K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache, quant_mode=N.QUANT_MUL_F32,
+                   k_scale=b.k_quant, v_scale=b.v_quant, scale_per_head=True)
+        o = torch.empty_like(b.q)
+        ws = torch.zeros(64 << 20, dtype=torch.uint8, device=dev)
+
+        def pstep(b=b, o=o, ws=ws, cfg=cfg):
+            K.paged_prefill(b.q, b.cu_seqlens, b.prior, b.max_seqlen_q, b.k_cache, b.v_cache,
+                            b.block_table, scale=cfg.head_dim ** -0.5, k_dequant=b.k_dequant,
+                            v_dequant=b.v_dequant, out=o, workspace=ws)
+
+        us = _graph_us(pstep, dev, reps)
+        fl = W.prefill_flops(b)
+        tf = fl / (us * 1e-6) / 1e12
+        out[name] = {"us_per_call": round(us, 2), "flops": fl, "tflops": round(tf, 1),
+                     "bound": "mfma", "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+        del b
+    m = W.make_mixed_batch(dev)
+    db, pb = m.decode, m.prefill
+    dws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    pws = torch.zeros(64 << 20, dtype=torch.uint8, device=dev)
+
+    def mstep():
+        mixed_batch_attention(
+            m.k_cache, m.v_cache, q_decode=db.q, k_decode=db.k_new, v_decode=db.v_new,
+            decode_block_table=db.block_table, decode_pos_ids=db.pos, decode_slots=db.slots,
+            q_prefill=pb.q, k_prefill=pb.k_new, v_prefill=pb.v_new, prefill_slots=pb.slots,
+            prefill_cu_seqlens=pb.cu_seqlens, prefill_prior=pb.prior,
+            prefill_block_table=pb.block_table, max_seqlen_q=pb.max_seqlen_q,
+            decode_workspace=dws, prefill_workspace=pws)
+
+    us = _graph_us(mstep, dev, reps)
+    nbytes = W.decode_bytes(db) + W.prefill_bytes(pb)
+    fl = W.prefill_flops(pb)
+    floor_us = max(nbytes / (HBM_PEAK_GBS * 1e9), fl / (BF16_PEAK_TFLOPS * 1e12)) * 1e6
+    out["llama3_8b_mixed_4x512_plus_60_decode"] = {
+        "us_per_call": round(us, 2), "algorithmic_bytes": nbytes, "flops": fl,
+        "floor_us": round(floor_us, 1), "frac_of_floor": round(floor_us / us, 4),
+        "dominant": "hbm" if nbytes / (HBM_PEAK_GBS * 1e9) >= fl / (BF16_PEAK_TFLOPS * 1e12)
+        else "mfma"}
+    return out
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+    return platform.processor() or "unknown"
+
+
 def cpu_baseline(gpu_batch, rows=16):
     """The oracle (CPU restatement of the reference torch decode path,
     attention_decode.py:653-1182, mask pre-generated as the Llama caller
@@ -176,6 +311,7 @@ def cpu_baseline(gpu_batch, rows=16):
         "value": round(nbytes / t / 1e9, 4),
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
+        "cpu_model": _cpu_model(),
         "kind": "port",
         "sample": (f"first {rows} of {B} batch rows of the Llama-3-8B decode batch; "
                    f"{t * 1e3:.1f} ms per call, median of 3 after 1 warm-up; "
@@ -268,6 +404,9 @@ def main() -> int:
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="first run a plain device-to-device copy of this many MiB three "
                          "times (the reference kernel for scaling HBM byte counters)")
+    ap.add_argument("--no-secondary", action="store_true",
+                    help="skip the other workloads (GPT-OSS decode, FP8 decode and chunk, "
+                         "Llama-3.2-1B decode, mixed batch)")
     ap.add_argument("--qkv-epilogue", action="store_true",
                     help="time the QKV epilogue and row norm kernels instead (one JSON line "
                          "per kernel shape; not the headline metric)")
@@ -341,6 +480,8 @@ def main() -> int:
             "flops": pre["flops"],
         },
     }
+    if not args.no_secondary:
+        line["secondary"] = bench_secondary(dev, max(4, args.steps // 8))
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(dec["batch"], args.cpu_rows)
     else:

@@ -674,13 +674,27 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
 // by lane 4j + k/4, j = 0..3.  Lane (group gi, k) therefore addresses key
 // row base + k/4 and the 4 d values starting at 4 * (k % 4) of its group's
 // 16 columns, and receives 4 consecutive keys of column d = lane % 32.
+// Shape of the DMA kernel: waves per workgroup and stages of the copy ring.
+// 8 waves (256 rows) with a 3-stage ring fill a CU with one workgroup;
+// 4 waves (128 rows) with a 2-stage ring fit two workgroups per CU, whose
+// barriers are independent.
 constexpr int kDmaWaves = 8;
-constexpr int kDmaRows = kDmaWaves * kRowsW;  // 256 rows per workgroup
-constexpr int kDmaIds = 4096;                 // block ids staged in LDS
+constexpr int kDmaStages = 3;
+constexpr int dma_rows(int waves) { return waves * kRowsW; }
+constexpr int dma_ids(int waves) { return waves == 8 ? 4096 : 2048; }  // block ids in LDS
+constexpr int kDmaRows = dma_rows(kDmaWaves);
+constexpr int kDmaIds = dma_ids(kDmaWaves);
+// s_waitcnt immediate: vmcnt(n), expcnt and lgkmcnt not waited on
+constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+static_assert(waitcnt_vm(4) == 0xF74 && waitcnt_vm(0) == 0xF70, "vmcnt encoding");
 
-template <int D>
-__global__ __launch_bounds__(512, 1) void prefill_dma_kernel(PrefillKParams p) {
+template <int D, int WAVES, int STAGES>
+__global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(PrefillKParams p) {
   static_assert(D == 128, "256-byte rows");
+  static_assert((WAVES == 8 || WAVES == 4) && (STAGES == 2 || STAGES == 3), "ring shape");
+  constexpr int kDmaWaves = WAVES;
+  constexpr int kDmaRows = dma_rows(WAVES);
+  constexpr int kDmaIds = dma_ids(WAVES);
   constexpr int KSTEPS = D / 16;
   constexpr int DBLK = D / 32;
   constexpr int ROWB = D * 2;          // bytes per K/V row
@@ -691,7 +705,7 @@ __global__ __launch_bounds__(512, 1) void prefill_dma_kernel(PrefillKParams p) {
   typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
 
   __shared__ __attribute__((aligned(16))) int32_t ids_lds[kDmaIds];
-  __shared__ __attribute__((aligned(1024))) uint8_t kv_lds[3][2][TILEB];  // [stage][K, V]
+  __shared__ __attribute__((aligned(1024))) uint8_t kv_lds[STAGES][2][TILEB];  // [stage][K, V]
   // LDS addresses are handled as LDS pointers / integers only: a generic
   // pointer to shared memory carried through the loops would need the
   // aperture conversion at every use
@@ -922,30 +936,36 @@ __global__ __launch_bounds__(512, 1) void prefill_dma_kernel(PrefillKParams p) {
     }
   };
 
-  // ---- 3-stage ring.  At the top of a step this thread waits for its own
-  // copies of tile kt (those of tile kt + 64, issued later, may stay in
-  // flight: 2 * NJ instructions), then the barrier makes every thread's
-  // copies visible and guarantees that the stage of tile kt - 64, which the
-  // step refills, is no longer read.
+  // ---- copy ring of STAGES stages.  At the top of a step this thread waits
+  // for its own copies of tile kt (those of the tiles issued after it may
+  // stay in flight: 2 * NJ instructions per tile), then the barrier makes
+  // every thread's copies visible and guarantees that the stage of tile
+  // kt - 64, which the step refills, is no longer read.
   if (any_key) {
     const uint32_t lds0 = (uint32_t)(uintptr_t)kv_base;
     auto k_at = [&](int stg) { return lds0 + (uint32_t)(stg * 2 * TILEB); };
-    issue_tile(kt0, k_at(0), k_at(0) + TILEB);
-    if (kt0 + kKT <= kt_last) issue_tile(kt0 + kKT, k_at(1), k_at(1) + TILEB);
+    constexpr int kAhead = STAGES - 1;  // tiles in flight beside the one computed
+#pragma unroll
+    for (int i = 0; i < kAhead; ++i)
+      if (kt0 + i * kKT <= kt_last) issue_tile(kt0 + i * kKT, k_at(i), k_at(i) + TILEB);
     int st = 0;
     for (int kt = kt0; kt <= kt_last; kt += kKT) {
-      static_assert(2 * NJ == 4, "vmcnt immediate below assumes 4 copies per tile");
-      if (kt + kKT <= kt_last)
-        __builtin_amdgcn_s_waitcnt(0xF74);  // vmcnt(4) expcnt(7) lgkmcnt(15)
-      else
-        __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
+      if constexpr (STAGES == 3) {
+        if (kt + kKT <= kt_last)
+          __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * NJ));  // the next tile stays in flight
+        else
+          __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      } else {
+        __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      }
       asm volatile("" ::: "memory");
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
-      const int st2 = st >= 1 ? st - 1 : 2;  // (st + 2) % 3
-      if (kt + 2 * kKT <= kt_last) issue_tile(kt + 2 * kKT, k_at(st2), k_at(st2) + TILEB);
+      const int st_n = st == 0 ? STAGES - 1 : st - 1;  // (st + kAhead) % STAGES
+      if (kt + kAhead * kKT <= kt_last)
+        issue_tile(kt + kAhead * kKT, k_at(st_n), k_at(st_n) + TILEB);
       compute_tile(kt, kv_base + st * 2 * TILEB, kv_base + st * 2 * TILEB + TILEB);
-      st = st == 2 ? 0 : st + 1;
+      st = st == STAGES - 1 ? 0 : st + 1;
     }
   }
 
@@ -1062,7 +1082,7 @@ PrefillPlan plan_prefill(const mia_prefill_args &a) {
   const int64_t s_ctx = (int64_t)a.blocks_per_seq * a.block_size;
   const int64_t base_wgs =
       (int64_t)((pl.rows_max + pl.rows_wg - 1) / pl.rows_wg) * a.num_kv_heads * a.num_seqs;
-  const int slots = device_cus() * (pl.dma ? 1 : 2);
+  const int slots = device_cus() * (pl.dma ? 8 / kDmaWaves : 2);
   pl.slots = slots;
   int64_t ks = a.split_tokens;
   if (ks <= 0 && (a.non_causal || a.bound_min)) {
@@ -1157,7 +1177,8 @@ int launch_paged_prefill(const mia_prefill_args &a, const PrefillPlan &pl, hipSt
   const dim3 grid((unsigned)((pl.rows_max + pl.rows_wg - 1) / pl.rows_wg),
                   (unsigned)a.num_kv_heads, (unsigned)(pl.nsplit * a.num_seqs));
   if (pl.dma) {
-    hipLaunchKernelGGL((prefill_dma_kernel<128>), grid, dim3(kDmaWaves * 64), 0, s, kp);
+    hipLaunchKernelGGL((prefill_dma_kernel<128, kDmaWaves, kDmaStages>), grid,
+                       dim3(kDmaWaves * 64), 0, s, kp);
   } else if (a.head_dim == 128) {
     if (a.k_packed) hipLaunchKernelGGL((prefill_kernel<128, true, true>), grid, dim3(256), 0, s, kp);
     else if (fp8) hipLaunchKernelGGL((prefill_kernel<128, true, false>), grid, dim3(256), 0, s, kp);

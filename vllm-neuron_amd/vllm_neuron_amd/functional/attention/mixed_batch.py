@@ -12,6 +12,11 @@ composition this function implements and is tested against:
 
 Here the prefill sequences run as one varlen launch and the decode rows as
 one split-K launch, on the caller's stream, sharing the same paged cache.
+The two launches run back to back: the decode is HBM-bound and needs every
+CU to approach the memory roofline (at the Llama-3-8B mixed shape its 60
+rows take 525 / 299 / 203 us on 64 / 128 / 256 CUs), and the two kernels
+run concurrently on complementary CU-masked streams measured 445-510 us
+against 295 us back to back, so the GPU is not split between them.
 """
 from __future__ import annotations
 
@@ -54,6 +59,7 @@ def mixed_batch_attention(
     k_dequant_scale: Optional[Tensor] = None,
     v_dequant_scale: Optional[Tensor] = None,
     decode_workspace: Optional[Tensor] = None,
+    prefill_workspace: Optional[Tensor] = None,
 ) -> Tuple[Optional[Tensor], Optional[Tensor]]:
     """Returns ``(out_decode [Bd, S_tkg, Hq, d], out_prefill [Tp, Hq, d])``."""
     d = V_cache.shape[-1]
@@ -74,7 +80,7 @@ def mixed_batch_attention(
             q_prefill, prefill_cu_seqlens, prefill_prior, max_seqlen_q,
             K_cache, V_cache, prefill_block_table, scale=scale,
             sliding_window=sliding_window, sink=sink,
-            k_dequant=k_dequant_scale, v_dequant=v_dequant_scale)
+            k_dequant=k_dequant_scale, v_dequant=v_dequant_scale, workspace=prefill_workspace)
 
     out_d = None
     if q_decode is not None:
