@@ -404,6 +404,8 @@ def main() -> int:
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="first run a plain device-to-device copy of this many MiB three "
                          "times (the reference kernel for scaling HBM byte counters)")
+    ap.add_argument("--only", choices=("decode", "prefill"), default=None,
+                    help="run one leg only (for profiler runs) and print its timing as JSON")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the other workloads (GPT-OSS decode, FP8 decode and chunk, "
                          "Llama-3.2-1B decode, mixed batch)")
@@ -433,7 +435,18 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.only == "prefill":
+        pre = bench_prefill(dev, max(5, args.steps // 2), max(2, args.warmup // 2))
+        print(json.dumps({"workload": "llama3_8b_chunked_prefill_4x512_prior0-4096",
+                          "us_per_call": round(pre["ms"] * 1e3, 2),
+                          "tflops": round(pre["tflops"], 2)}), flush=True)
+        return 0
     dec = bench_decode(dev, args.steps, args.warmup)
+    if args.only == "decode":
+        print(json.dumps({"workload": "llama3_8b_paged_decode_b64_ctx512-8192",
+                          "ms_per_step": round(dec["ms_step"], 4),
+                          "split_avg_us": round(dec["split_avg_ms"] * 1e3, 2)}), flush=True)
+        return 0
     pre = bench_prefill(dev, max(5, args.steps // 2), max(2, args.warmup // 2))
     cfg = dec["cfg"]
     value = dec["total_bytes"] / (dec["ms_step"] * 1e-3) / 1e9
