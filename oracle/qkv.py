@@ -183,3 +183,52 @@ def ref_decode_qkv(X, W_qkv, q_heads, kv_heads, d_head, *, bias_qkv=None, rmsnor
         eps, wq, wk = qk_post
         q, k = _rms_rows(q, eps, wq, mean=True), _rms_rows(k, eps, wk, mean=True)
     return q, k, v
+
+
+def f64_decode_qkv(X, W_qkv, q_heads, kv_heads, d_head, *, bias_qkv=None, rmsnorm_X=None,
+                   qk_pre=None, qk_post=None, cos=None, sin=None, contiguous=True):
+    """Float64 statement of decode stages 1-6.5 (the math of
+    attention_decode.py:800-890 without its bf16 rounding points): input RMS
+    norm, projection with bias, QK RMS norm before and after RoPE, RoPE as an
+    explicit rotation of each channel pair -- (i, i + d/2) half split,
+    (2i, 2i + 1) interleaved -- by the angle of cos/sin ``[d/2, B, S]``.
+    Arguments as ``ref_decode_qkv``; returns float64 q ``[B, S, Hq, d]``, k
+    and v ``[B, S, Hkv, d]``."""
+    B, S, H = X.shape
+    hid = X.double()
+    if rmsnorm_X is not None:
+        eps, g, da = rmsnorm_X
+        n = da or H
+        hid = hid * torch.rsqrt(hid.pow(2).sum(-1, keepdim=True) / n + eps)
+        if g is not None:
+            hid = hid * g.double().reshape(-1)
+    qkv = hid @ W_qkv.double()
+    if bias_qkv is not None:
+        qkv = qkv + bias_qkv.double().reshape(-1)
+    qe, ke = q_heads * d_head, (q_heads + kv_heads) * d_head
+    q = qkv[..., :qe].reshape(B, S, q_heads, d_head)
+    k = qkv[..., qe:ke].reshape(B, S, kv_heads, d_head)
+    v = qkv[..., ke:].reshape(B, S, kv_heads, d_head)
+
+    def rms(t, w, eps):
+        t = t * torch.rsqrt(t.pow(2).mean(-1, keepdim=True) + eps)
+        return t if w is None else t * w.double().reshape(-1)
+
+    if qk_pre is not None:
+        eps, wq, wk = qk_pre
+        q, k = rms(q, wq, eps), rms(k, wk, eps)
+    if cos is not None and sin is not None:
+        c = cos.double().permute(1, 2, 0).unsqueeze(2)   # [B, S, 1, d/2]
+        sn = sin.double().permute(1, 2, 0).unsqueeze(2)
+        h = d_head // 2
+
+        def rope(t):
+            a, b = (t[..., :h], t[..., h:]) if contiguous else (t[..., 0::2], t[..., 1::2])
+            ra, rb = a * c - b * sn, b * c + a * sn
+            return torch.cat([ra, rb], -1) if contiguous else torch.stack([ra, rb], -1).flatten(-2)
+
+        q, k = rope(q), rope(k)
+    if qk_post is not None:
+        eps, wq, wk = qk_post
+        q, k = rms(q, wq, eps), rms(k, wk, eps)
+    return q, k, v

@@ -20,6 +20,8 @@ import math
 import torch
 import torch.nn.functional as F
 
+from . import dense as _dense
+
 
 def rope_rotate(x, cos, sin):
     """Pairwise rotation: (a, b) -> (a cos - b sin, b cos + a sin) with
@@ -119,3 +121,37 @@ def make_rope(B, S, d, prior, base=10000.0):
     cos = torch.cat([ang.cos(), ang.cos()], -1).float().unsqueeze(0).expand(B, S, d)
     sin = torch.cat([ang.sin(), ang.sin()], -1).float().unsqueeze(0).expand(B, S, d)
     return cos.contiguous(), sin.contiguous()
+
+
+def f64_swa_fused(a):
+    """Float64 statement of the fused SWA layer, written apart from
+    ``ref_swa_fused``: the projection, the pairwise RoPE rotation, the
+    float64 textbook attention of ``oracle.dense`` (window, prior rows, sink)
+    and the output projection.  ``a`` holds ``ref_swa_fused``'s keyword
+    arguments with a bf16 cache (or an FP8 cache dequantised to floats in
+    the unpacked layout).  Returns the float64 output ``[B, S, H]``."""
+    x = a["hidden_states"].double()
+    B, S, H = x.shape
+    Hq, Hkv, d, bs, W = a["num_q_heads"], a["num_kv_heads"], a["d_head"], a["block_size"], \
+        a["sliding_window"]
+    P = int(a["prior_tokens"].reshape(-1)[0])
+    qkv = x @ a["qkv_weight"].double() + a["qkv_bias"].double()
+    q = qkv[..., :Hq * d].reshape(B, S, Hq, d)
+    k = qkv[..., Hq * d:(Hq + Hkv) * d].reshape(B, S, Hkv, d)
+    v = qkv[..., (Hq + Hkv) * d:].reshape(B, S, Hkv, d)
+    cos, sin = a["cos_cache"].double().unsqueeze(2), a["sin_cache"].double().unsqueeze(2)
+    q = rope_rotate(q, cos, sin) * a["scale"]
+    k = rope_rotate(k, cos, sin)
+    outs = []
+    for b in range(B):
+        kp = torch.stack([a["k_cache"][a["block_tables"][b, t // bs], :, t % bs].double()
+                          for t in range(P)]) if P else torch.zeros(0, Hkv, d, dtype=torch.float64)
+        vp = torch.stack([a["v_cache"][a["block_tables"][b, t // bs], :, t % bs].double()
+                          for t in range(P)]) if P else torch.zeros(0, Hkv, d, dtype=torch.float64)
+        kk = torch.cat([kp, k[b]], 0).transpose(0, 1)   # [Hkv, P+S, d]
+        vv = torch.cat([vp, v[b]], 0).transpose(0, 1)
+        att = _dense.textbook_attention(q[b].transpose(0, 1), kk, vv, 1.0, causal=True,
+                                        window=W, prior=P, sink=a["sink"][b])  # [Hq, S, d]
+        outs.append(att.transpose(0, 1).reshape(S, Hq * d) @ a["op_weight"].double()
+                    + a["op_bias"].double())
+    return torch.stack(outs)

@@ -195,3 +195,38 @@ def test_decode_rope_is_the_pairwise_rotation(contiguous):
     # rotation by the angle's negative undoes it
     q2, _ = OQ._rope_decode(qr, kr, cos, -sin, contiguous)
     assert (q2 - q).abs().max().item() < 1e-12
+
+
+@pytest.mark.parametrize("contiguous", [True, False])
+def test_f64_decode_stages_statement(contiguous):
+    """The float64 statement of decode stages 1-6.5 used as the GPU bar:
+    with no norms and an identity projection it is the split of X rotated by
+    the (element-loop pinned) RoPE restatement, exactly; with norms, bias and
+    real weights it stays within the bf16 tolerance of the op-for-op
+    restatement, whose bf16 rounding points it leaves out."""
+    B, S, H, Hq, Hkv, d = 2, 1, 128, 4, 2, 16
+    g = torch.Generator().manual_seed(31)
+    fused = (Hq + 2 * Hkv) * d
+    X = torch.randn(B, S, fused, generator=g).to(bf)
+    cos = torch.randn(d // 2, B, S, generator=g).clamp(-1, 1).double()
+    sin = torch.randn(d // 2, B, S, generator=g).clamp(-1, 1).double()
+    q, k, v = OQ.f64_decode_qkv(X, torch.eye(fused, dtype=bf), Hq, Hkv, d, cos=cos, sin=sin,
+                                contiguous=contiguous)
+    x = X.double()
+    q0 = x[..., :Hq * d].reshape(B, S, Hq, d).transpose(1, 2)
+    k0 = x[..., Hq * d:(Hq + Hkv) * d].reshape(B, S, Hkv, d).transpose(1, 2)
+    qr, kr = OQ._rope_decode(q0, k0, cos, sin, contiguous)
+    assert torch.equal(q, qr.transpose(1, 2)) and torch.equal(k, kr.transpose(1, 2))
+    assert torch.equal(v, x[..., (Hq + Hkv) * d:].reshape(B, S, Hkv, d))
+    # norms, bias and real weights: within bf16 tolerance of the restatement
+    X = torch.randn(B, S, H, generator=g).to(bf)
+    W = (torch.randn(H, fused, generator=g) / H ** 0.5).to(bf)
+    bias = (torch.randn(fused, generator=g) * 0.1).to(bf)
+    gx = (torch.rand(H, generator=g) + 0.5).to(bf)
+    wq, wk = torch.rand(1, d, generator=g) + 0.5, torch.rand(1, d, generator=g) + 0.5
+    kw = dict(bias_qkv=bias, rmsnorm_X=(1e-5, gx, None), qk_pre=(1e-6, wq, wk),
+              qk_post=(1e-5, wk, wq), cos=cos.float(), sin=sin.float(), contiguous=contiguous)
+    q64, k64, v64 = OQ.f64_decode_qkv(X, W, Hq, Hkv, d, **kw)
+    qb, kb, vb = OQ.ref_decode_qkv(X, W, Hq, Hkv, d, **kw)
+    for a, b_ in ((q64, qb), (k64, kb), (v64, vb)):
+        assert (a - b_.transpose(1, 2).double()).abs().max().item() <= 5e-2 * max(1.0, a.abs().max().item())

@@ -59,41 +59,12 @@ def test_rope_is_a_pairwise_rotation():
     assert torch.equal(OS._apply_rope(x[:1, :1], c0, s0), x[:1, :1])
 
 
-def _independent(a):
-    """float64 statement of the layer without the restatement's code path."""
-    x = a["hidden_states"].double()
-    B, S, H = x.shape
-    Hq, Hkv, d, bs, W = a["num_q_heads"], a["num_kv_heads"], a["d_head"], a["block_size"], \
-        a["sliding_window"]
-    P = int(a["prior_tokens"].reshape(-1)[0])
-    qkv = x @ a["qkv_weight"].double() + a["qkv_bias"].double()
-    q = qkv[..., :Hq * d].reshape(B, S, Hq, d)
-    k = qkv[..., Hq * d:(Hq + Hkv) * d].reshape(B, S, Hkv, d)
-    v = qkv[..., (Hq + Hkv) * d:].reshape(B, S, Hkv, d)
-    cos, sin = a["cos_cache"].double().unsqueeze(2), a["sin_cache"].double().unsqueeze(2)
-    q = OS.rope_rotate(q, cos, sin) * a["scale"]
-    k = OS.rope_rotate(k, cos, sin)
-    outs = []
-    for b in range(B):
-        kp = torch.stack([a["k_cache"][a["block_tables"][b, t // bs], :, t % bs].double()
-                          for t in range(P)]) if P else torch.zeros(0, Hkv, d, dtype=torch.float64)
-        vp = torch.stack([a["v_cache"][a["block_tables"][b, t // bs], :, t % bs].double()
-                          for t in range(P)]) if P else torch.zeros(0, Hkv, d, dtype=torch.float64)
-        kk = torch.cat([kp, k[b]], 0).transpose(0, 1)   # [Hkv, P+S, d]
-        vv = torch.cat([vp, v[b]], 0).transpose(0, 1)
-        att = OD.textbook_attention(q[b].transpose(0, 1), kk, vv, 1.0, causal=True, window=W,
-                                    prior=P, sink=a["sink"][b])          # [Hq, S, d]
-        outs.append(att.transpose(0, 1).reshape(S, Hq * d) @ a["op_weight"].double()
-                    + a["op_bias"].double())
-    return torch.stack(outs)
-
-
 @pytest.mark.parametrize("prior,W,B", [(21, 12, 1), (0, 16, 2), (48, 5, 1), (7, 16, 2)])
 def test_restatement_vs_independent_layer(prior, W, B):
     a = _layer(B=B, prior=prior, W=W, seed=prior + W)
     ref_in = {k: (v.clone() if torch.is_tensor(v) else v) for k, v in a.items()}
     out, _, _ = OS.ref_swa_fused(**ref_in)
-    exp = _independent(a)
+    exp = OS.f64_swa_fused(a)
     # the restatement rounds the output to bf16 at the end only
     assert (out.double() - exp).abs().max().item() <= 2e-2
 
