@@ -215,20 +215,33 @@ MIA_DEV int split_keys(const PrefillKParams &p) {
   return p.nsplit <= 1 ? (1 << 30) : p.ksplit;
 }
 
+// Sequence metadata of a work item: first token, new tokens, prior tokens.
+struct SeqInfo {
+  int q_begin, S_q, prior, pad;
+};
+MIA_DEV SeqInfo load_seq(const PrefillKParams &p, int seq) {
+  SeqInfo si;
+  si.q_begin = p.cu[seq];
+  si.S_q = p.cu[seq + 1] - si.q_begin;
+  si.prior = p.prior[seq];
+  si.pad = 0;
+  return si;
+}
+
 // Key tiles (plus one for the fixed per-workgroup cost) of work item
 // (row tile rt, group g = kv head + Hkv * (chunk * num_seqs + sequence));
 // 0 for an item that exits at once (rows past the sequence, or a chunk past
 // the row tile's key range).  The kv head does not change the cost.
-MIA_DEV int item_cost(const PrefillKParams &p, int rt, int g) {
+MIA_DEV int item_cost(const PrefillKParams &p, int rt, int g, SeqInfo &si) {
   const int z = g / p.Hkv;
   const int sp = z / p.num_seqs;
   const int seq = z - sp * p.num_seqs;
-  const int q_begin = p.cu[seq];
-  const int S_q = p.cu[seq + 1] - q_begin;
+  si = load_seq(p, seq);
+  const int S_q = si.S_q;
   const int row0 = rt * p.rows_wg;
   if (row0 >= S_q * p.G) return 0;
   const int ksplit = split_keys(p);
-  const KeyRange kr = wg_key_range(p, seq, p.prior[seq], S_q, row0, ksplit);
+  const KeyRange kr = wg_key_range(p, seq, si.prior, S_q, row0, ksplit);
   if (sp >= kr.n_sp) return 0;
   if (!kr.any) return 1;
   int kt0 = kr.kt0, kt_last = kr.kt_last;
@@ -259,42 +272,56 @@ constexpr uint32_t kRankMax = 512;  // items per XCD ranked at most
 // holds cap ints of 16-byte aligned LDS.  Falls back to xcd_tile when the
 // host did not ask for ranking, the group count is not a multiple of 8 or
 // an XCD has more items than the scratch or kRankMax.
-MIA_DEV uint3 ranked_tile(const PrefillKParams &p, int *scratch, int cap) {
+MIA_DEV uint3 ranked_tile(const PrefillKParams &p, int *scratch, int cap, SeqInfo &info) {
   constexpr uint32_t X = 8;
   const uint32_t R = gridDim.x;
   const uint32_t groups = gridDim.y * gridDim.z;
   const uint32_t n_x = R * (groups / X);  // items per XCD
-  const uint32_t n4 = (n_x + 3) & ~3u;     // costs padded to 16-byte groups
-  if (!p.rank_items || groups % X != 0 || n4 + 1 > (uint32_t)cap || n_x > kRankMax)
-    return xcd_tile();
+  // LDS: costs [0, n_x), the chosen item at [n_x], item metadata from mo
+  const uint32_t mo = (n_x + 4) & ~3u;
+  if (!p.rank_items || groups % X != 0 || mo + 4 * n_x > (uint32_t)cap || n_x > kRankMax ||
+      n_x > blockDim.x) {
+    const uint3 t = xcd_tile();
+    info = load_seq(p, (int)(t.z % (uint32_t)p.num_seqs));
+    return t;
+  }
   const uint32_t L = blockIdx.x + R * (blockIdx.y + gridDim.y * blockIdx.z);
   const uint32_t x = L % X, k = L / X;
-  // item j of XCD x: row tile j % R of group x + 8 (j / R); padding costs -1
-  // rank nothing (real costs are >= 0)
-  for (uint32_t j = threadIdx.x; j < n4; j += blockDim.x)
-    scratch[j] = j < n_x ? item_cost(p, (int)(j % R), (int)(x + X * (j / R))) : -1;
-  __syncthreads();
-  // rank of item j: items of higher cost, or of equal cost and lower index.
-  // Costs are read 4 per 16-byte LDS load, 4 loads in flight.
   typedef int i32x4_t __attribute__((ext_vector_type(4)));
-  const i32x4_t *c4 = reinterpret_cast<const i32x4_t *>(scratch);
-  for (uint32_t j = threadIdx.x; j < n_x; j += blockDim.x) {
-    const int c = scratch[j];
-    uint32_t rank = 0;
-#pragma unroll 4
-    for (uint32_t i4 = 0; i4 < n4 / 4; ++i4) {
-      const i32x4_t ci = c4[i4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        rank += (ci[e] > c) || (ci[e] == c && 4 * i4 + e < j);
-    }
-    if (rank == k) scratch[n4] = (int)j;
+  // item j of XCD x: row tile j % R of group x + 8 (j / R); thread j
+  // computes its cost and metadata
+  const uint32_t tid = threadIdx.x;
+  if (tid < n_x) {
+    SeqInfo mine;
+    scratch[tid] = item_cost(p, (int)(tid % R), (int)(x + X * (tid / R)), mine);
+    *reinterpret_cast<i32x4_t *>(scratch + mo + 4 * tid) =
+        i32x4_t{mine.q_begin, mine.S_q, mine.prior, 0};
   }
   __syncthreads();
-  const uint32_t j = (uint32_t)scratch[n4];
-  const uint32_t g = x + X * (j / R);
+  // rank of item j: items of higher cost, or of equal cost and lower index,
+  // counted 64 at a time with a ballot; each wave ranks every nw-th item
+  const uint32_t lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
+  for (uint32_t j = wv; j < n_x; j += nw) {
+    const int cj = scratch[j];
+    uint32_t rank = 0;
+    for (uint32_t i0 = 0; i0 < n_x; i0 += 64) {
+      const uint32_t i = i0 + lane;
+      const int ci = i < n_x ? scratch[i] : -1;  // costs are >= 0
+      rank += (uint32_t)__builtin_popcountll(
+          __builtin_amdgcn_ballot_w64(ci > cj || (ci == cj && i < j)));
+    }
+    if (rank == k && lane == 0) scratch[n_x] = (int)j;
+  }
+  __syncthreads();
+  const uint32_t jj = (uint32_t)scratch[n_x];
+  const i32x4_t w = *reinterpret_cast<const i32x4_t *>(scratch + mo + 4 * jj);
+  info.q_begin = w[0];
+  info.S_q = w[1];
+  info.prior = w[2];
+  info.pad = 0;
+  const uint32_t g = x + X * (jj / R);
   uint3 t;
-  t.x = j % R;
+  t.x = jj % R;
   t.y = g % gridDim.y;
   t.z = g / gridDim.y;
   return t;
@@ -382,6 +409,82 @@ struct Chunk8<true> {
   static MIA_DEV u32x4_t bf16(raw_t r) { return e4m3fn_x8_to_bf16_scaled(r); }
 };
 
+// ---------------------------------------------------------------------------
+// online softmax shared by the attention kernels
+// ---------------------------------------------------------------------------
+// Q pre-multiplied by the softmax scale in log2 units, rounded to bf16: the
+// QK MFMA then yields scaled scores and the softmax needs no multiply.
+MIA_DEV bf16x8_t scale_q8(u32x4_t w, float scale) {
+  u32x4_t o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    o[i] = pack2_bf16(__uint_as_float(w[i] << 16) * scale,
+                      __uint_as_float(w[i] & 0xffff0000u) * scale);
+  return __builtin_bit_cast(bf16x8_t, o);
+}
+
+// Running maximum of a row (log2 units).  negm holds -m in every element and
+// is the accumulator input of the first QK MFMA of a tile, so the MFMA
+// yields s - m directly; m is 0 until the row's first visible key sets it.
+struct RowMax {
+  float m = 0.f;
+  bool set = false;
+  f32x16_t negm = {};
+  // the row's maximum for the epilogue (-inf: no visible key)
+  MIA_DEV float final_max() const { return set ? m : -INFINITY; }
+};
+
+// One tile of the online softmax over sacc = s - m (masked keys -inf) of
+// the lane's row: probabilities as bf16 pairs into pk, acc_o rescaled when
+// the maximum moves, returns the updated partial sum of the lane.
+// Lazy rescaling: the maximum only moves when a score exceeds it by more
+// than 8 (log2 units), so probabilities stay below 2^8 and the accumulators
+// are rescaled only on such tiles; the first visible key of a row always
+// sets it.  The sum adds the bf16-rounded probabilities the PV product uses
+// (v_dot2c_f32_bf16 with (1, 1)).
+template <int DBLK>
+MIA_DEV float softmax_tile(f32x16_t (&sacc)[2], RowMax &rm, f32x16_t (&acc_o)[DBLK],
+                           float l_run, uint32_t (&pk)[2][8]) {
+  float mx = -INFINITY;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[kb][e]);
+  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // the other k-group of the row
+  const bool bump = rm.set ? (mx > 8.0f) : (mx > -INFINITY);
+  if (__builtin_amdgcn_ballot_w64(bump)) {
+    const float delta = bump ? mx : 0.f;
+    // before the first visible key acc_o and l_run are 0: no rescale
+    const float alpha = rm.set ? __builtin_amdgcn_exp2f(-delta) : 1.0f;
+    rm.m += delta;
+    rm.set = rm.set || bump;
+    l_run *= alpha;
+#pragma unroll
+    for (int i = 0; i < DBLK; ++i)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc_o[i][e] *= alpha;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) sacc[kb][e] -= delta;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) rm.negm[e] = -rm.m;
+  }
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  const bf16x2_t ones = {(__bf16)1.0f, (__bf16)1.0f};
+  float psum = 0.f;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int e = 0; e < 16; e += 2) {
+      const float p0 = __builtin_amdgcn_exp2f(sacc[kb][e]);
+      const float p1 = __builtin_amdgcn_exp2f(sacc[kb][e + 1]);
+      pk[kb][e >> 1] = pack2_bf16(p0, p1);
+      psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, pk[kb][e >> 1]), ones,
+                                             psum, false);
+    }
+  return l_run + psum;
+}
 
 // PK: the K cache is in the packed FP8 layout (FP8 only).
 template <int D, bool FP8, bool PK>
@@ -402,20 +505,20 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[D * VROW];
 
   // heaviest work item first (the K tile buffer is free until the loop)
-  const uint3 tile = ranked_tile(p, reinterpret_cast<int *>(k_lds),
-                                 (int)(sizeof(k_lds) / sizeof(int)));
+  SeqInfo si;
+  const uint3 tile = ranked_tile(p, reinterpret_cast<int *>(k_lds), (int)(sizeof(k_lds) / 4), si);
   __syncthreads();  // the ranking scratch is read before the first K tile store
   const int sp = tile.z / p.num_seqs;  // key chunk of a split row tile
   const int seq = tile.z - sp * p.num_seqs;
   const int h = tile.y;
   const int G = p.G;
-  const int q_begin = p.cu[seq];
-  const int S_q = p.cu[seq + 1] - q_begin;
+  const int q_begin = si.q_begin;
+  const int S_q = si.S_q;
   const int rows_total = S_q * G;
   const int row0 = tile.x * kRowsWG;
   if (row0 >= rows_total) return;
   const int ksplit = split_keys(p);
-  const int prior = p.prior[seq];
+  const int prior = si.prior;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -441,7 +544,10 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
   // no tile is loaded and every row outputs 0
   const bool any_key = kr.any;
 
-  // ---- Q^T fragments (B operand): lane holds Q[row rl][ks*16 + half*8 .. +8]
+  // ---- Q^T fragments (B operand): lane holds Q[row rl][ks*16 + half*8 .. +8],
+  // multiplied by the softmax scale (log2 units) and rounded to bf16, so the
+  // MFMA yields scaled scores
+  const float scale2 = p.scale_log2 * (p.k_deq ? p.k_deq[h] : 1.0f);
   bf16x8_t qf[KSTEPS];
   {
     const uint16_t *qp = p.q + (int64_t)(q_begin + (row_ok ? pos_r : 0)) * p.qs_t +
@@ -450,10 +556,9 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
     for (int ks = 0; ks < KSTEPS; ++ks) {
       u32x4_t w = {0u, 0u, 0u, 0u};  // zero query: uniform row, scores 0
       if (row_ok && !uni) w = *reinterpret_cast<const u32x4_t *>(qp + ks * 16 + half * 8);
-      qf[ks] = __builtin_bit_cast(bf16x8_t, w);
+      qf[ks] = scale_q8(w, scale2);
     }
   }
-  const float scale2 = p.scale_log2 * (p.k_deq ? p.k_deq[h] : 1.0f);
   const int64_t bt_row = (int64_t)seq * p.bt_s + (int64_t)h * p.bt_h;
 
   // ---- staging roles
@@ -549,7 +654,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
     }
   };
 
-  float m_run = -INFINITY;  // scaled (log2) domain, per row
+  RowMax rm;
   float l_run = 0.f;        // per lane partial sum
   f32x16_t acc_o[DBLK];
 #pragma unroll
@@ -575,18 +680,17 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
     const int32_t kph_nn = phys_of(kt_n + kKT + k_key);
     const int32_t vph_nn = phys_of(kt_n + kKT + vg * 4);
 
-    // ---- S^T = K . Q^T, two 32-key blocks
+    // ---- S^T = K . Q^T - m (log2 units), two 32-key blocks
     f32x16_t sacc[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int e = 0; e < 16; ++e) sacc[kb][e] = 0.f;
 #pragma unroll
       for (int ks = 0; ks < KSTEPS; ++ks) {
         const u32x4_t a = *reinterpret_cast<const u32x4_t *>(
             &k_lds[(kb * 32 + rl) * KROW + ks * 16 + half * 8]);
         sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                           qf[ks], sacc[kb], 0, 0, 0);
+                                                           qf[ks], ks == 0 ? rm.negm : sacc[kb],
+                                                           0, 0, 0);
       }
     }
     // lane value e of block kb: key kt + kb*32 + (e/4)*8 + half*4 + e%4
@@ -601,33 +705,9 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
           sacc[kb][e] = ok ? sacc[kb][e] : -INFINITY;
         }
     }
-    // ---- online softmax (log2 domain; scale folded into one fma)
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[kb][e]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m_run, mx * scale2);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    m_run = m_new;
-    float psum = 0.f;
+    // ---- online softmax (log2 domain)
     uint32_t pk[2][8];  // P^T as bf16 pairs, [block][dword]
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int e = 0; e < 16; e += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][e], scale2, -m_use));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][e + 1], scale2, -m_use));
-        psum += p0 + p1;
-        pk[kb][e >> 1] = pack2_bf16(p0, p1);
-      }
-    l_run = l_run * alpha + psum;
-#pragma unroll
-    for (int i = 0; i < DBLK; ++i)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) acc_o[i][e] *= alpha;
+    l_run = softmax_tile<DBLK>(sacc, rm, acc_o, l_run, pk);
 
     // ---- O^T += V^T . P^T: 4 k-steps of 16 keys (block kb, half kh)
 #pragma unroll
@@ -649,8 +729,8 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
   }
 
   // ---- finalize: lane holds O^T[d = db*32 + (e/4)*8 + half*4 + e%4][row rl]
-  finish_rows<D>(p, acc_o, m_run, l_run, row_ok, seq, h, hq, (int64_t)q_begin + pos_r, r, half,
-                 kr.n_sp, sp, (p.v_deq ? p.v_deq[h] : 1.0f) * (p.fp8 ? 256.0f : 1.0f));
+  finish_rows<D>(p, acc_o, rm.final_max(), l_run, row_ok, seq, h, hq, (int64_t)q_begin + pos_r,
+                 r, half, kr.n_sp, sp, (p.v_deq ? p.v_deq[h] : 1.0f) * (p.fp8 ? 256.0f : 1.0f));
 }
 
 // ---------------------------------------------------------------------------
@@ -704,7 +784,9 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
   typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
 
-  __shared__ __attribute__((aligned(16))) int32_t ids_lds[kDmaIds];
+  // byte offset of each block of the workgroup's key range (K and V share
+  // the block and token strides on this path)
+  __shared__ __attribute__((aligned(16))) int64_t offs_lds[kDmaIds];
   __shared__ __attribute__((aligned(1024))) uint8_t kv_lds[STAGES][2][TILEB];  // [stage][K, V]
   // LDS addresses are handled as LDS pointers / integers only: a generic
   // pointer to shared memory carried through the loops would need the
@@ -712,19 +794,20 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   lds_u8_t *const kv_base = (lds_u8_t *)&kv_lds[0][0][0];
 
   // heaviest work item first (the block-id buffer is free until it is filled)
-  const uint3 tile = ranked_tile(p, ids_lds, kDmaIds);
+  SeqInfo si;
+  const uint3 tile = ranked_tile(p, reinterpret_cast<int *>(offs_lds), 2 * kDmaIds, si);
   __syncthreads();  // the ranking scratch is read before the block ids land
   const int sp = tile.z / p.num_seqs;  // key chunk of a split row tile
   const int seq = tile.z - sp * p.num_seqs;
   const int h = tile.y;
   const int G = p.G;
-  const int q_begin = p.cu[seq];
-  const int S_q = p.cu[seq + 1] - q_begin;
+  const int q_begin = si.q_begin;
+  const int S_q = si.S_q;
   const int rows_total = S_q * G;
   const int row0 = tile.x * kDmaRows;
   if (row0 >= rows_total) return;
   const int ksplit = split_keys(p);
-  const int prior = p.prior[seq];
+  const int prior = si.prior;
   const int tid = threadIdx.x;
   const int wave = readfirstlane(tid >> 6);
   const int lane = tid & 63;
@@ -752,23 +835,19 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
     kt_last = min(kt_last, c * ksplit + ksplit - kKT);
   }
 
-  bf16x8_t qf[KSTEPS];
+  // Q pre-multiplied by the softmax scale (log2 units) and rounded to bf16,
+  // so that the MFMA yields scaled scores and the softmax needs no multiply
+  const float scale2 = p.scale_log2 * (p.k_deq ? p.k_deq[h] : 1.0f);
+  u32x4_t qw[KSTEPS];  // raw bf16 Q, scaled once the block ids are staged
   {
     const uint16_t *qp = p.q + (int64_t)(q_begin + (row_ok ? pos_r : 0)) * p.qs_t +
                          (int64_t)(row_ok ? hq : 0) * p.qs_h;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) {
-      u32x4_t w = {0u, 0u, 0u, 0u};  // zero query: uniform row, scores 0
-      if (row_ok && !uni) w = *reinterpret_cast<const u32x4_t *>(qp + ks * 16 + half * 8);
-      qf[ks] = __builtin_bit_cast(bf16x8_t, w);
+      qw[ks] = u32x4_t{0u, 0u, 0u, 0u};  // zero query: uniform row, scores 0
+      if (row_ok && !uni) qw[ks] = *reinterpret_cast<const u32x4_t *>(qp + ks * 16 + half * 8);
     }
-    // wait for Q here, before the copy ring starts: a wait placed by the
-    // compiler inside the loop would also drain the in-flight copies
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) asm volatile("" ::"v"(qf[ks]));
   }
-  const float scale2 = p.scale_log2 * (p.k_deq ? p.k_deq[h] : 1.0f);
-  asm volatile("" ::"v"(scale2));
   const int64_t bt_row = (int64_t)seq * p.bt_s + (int64_t)h * p.bt_h;
 
   // ---- block ids of blocks b_lo .. b_hi (clamped into the pool)
@@ -777,8 +856,18 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   if (any_key) {
     for (int i = tid; i <= b_hi - b_lo; i += blockDim.x) {
       int32_t v = p.bt[bt_row + (int64_t)(b_lo + i) * p.bt_j];
-      ids_lds[i] = v < 0 ? 0 : (v >= p.nb ? p.nb - 1 : v);
+      v = v < 0 ? 0 : (v >= p.nb ? p.nb - 1 : v);
+      offs_lds[i] = (int64_t)v * p.kc_blk * 2;
     }
+  }
+  // Q (its loads share the round trip of the block ids) scaled and rounded
+  // here, before the copy ring starts: a wait placed by the compiler inside
+  // the loop would also drain the in-flight copies
+  bf16x8_t qf[KSTEPS];
+#pragma unroll
+  for (int ks = 0; ks < KSTEPS; ++ks) {
+    qf[ks] = scale_q8(qw[ks], scale2);
+    asm volatile("" ::"v"(qf[ks]));
   }
   __syncthreads();
 
@@ -792,12 +881,15 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   const uint8_t *k_head = p.k_cache + (int64_t)h * p.kc_h * 2;
   const uint8_t *v_head = p.v_cache + (int64_t)h * p.vc_h * 2;
   int32_t k_lane[NJ], v_lane[NJ];  // bytes inside a block: < block_size * 256
+  int jblk[NJ];  // block of DMA j relative to the tile's first block (wave-uniform)
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
     const int row = 4 * (kDmaWaves * j + wave) + dma_r;
     const int roff = row % p.bs;
     k_lane[j] = roff * (int)p.kc_t * 2 + ((dma_s ^ (row & 15)) << 4);
-    v_lane[j] = roff * (int)p.vc_t * 2 + ((dma_s ^ ((row & 3) << 2)) << 4);
+    v_lane[j] = roff * (int)p.kc_t * 2 + ((dma_s ^ ((row & 3) << 2)) << 4);
+    // a 64-key tile starts a block (bs <= 64) or lies inside one (bs > 64)
+    jblk[j] = p.bs <= kKT ? (4 * (kDmaWaves * j + wave)) / p.bs : 0;
   }
   // One 16-byte-per-lane copy HBM -> LDS (global_load_lds_dwordx4): lane
   // data lands at lds_dst + 16 * lane.  Issued through inline assembly so
@@ -818,20 +910,22 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
         : "memory");
   };
   auto issue_tile = [&](int kt, uint32_t k_dst, uint32_t v_dst) {
-    const int ktoff = kt - (int)fdiv((uint32_t)kt, p.bs_div) * p.bs;  // kt % bs
+    const int kt_blk = (int)fdiv((uint32_t)kt, p.bs_div);
+    const int ktb = (kt - kt_blk * p.bs) * (int)p.kc_t * 2;  // (kt % bs) rows, in bytes
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int q = kDmaWaves * j + wave;
-      const int bi = min((int)fdiv((uint32_t)(kt + 4 * q), p.bs_div), p.nblk - 1) - b_lo;
-      const int32_t phys = readfirstlane(ids_lds[bi]);
-      const int64_t kb = ((int64_t)phys * p.kc_blk + (int64_t)ktoff * p.kc_t) * 2;
-      const int64_t vb = ((int64_t)phys * p.vc_blk + (int64_t)ktoff * p.vc_t) * 2;
-      dma16(k_head + kb + k_lane[j], k_dst + q * 1024);
-      dma16(v_head + vb + v_lane[j], v_dst + q * 1024);
+      const int bi = min(kt_blk + jblk[j], p.nblk - 1) - b_lo;
+      const int64_t o = offs_lds[bi];
+      const int64_t off =
+          (int64_t)(((uint64_t)(uint32_t)readfirstlane((int)(o >> 32)) << 32) |
+                    (uint32_t)readfirstlane((int)o)) + ktb;
+      dma16(k_head + off + k_lane[j], k_dst + q * 1024);
+      dma16(v_head + off + v_lane[j], v_dst + q * 1024);
     }
   };
 
-  float m_run = -INFINITY;
+  RowMax rm;
   float l_run = 0.f;
   f32x16_t acc_o[DBLK];
 #pragma unroll
@@ -845,13 +939,11 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   const int tr_row = half * 4 + (tr_k >> 2);
 
   auto compute_tile = [&](int kt, const lds_u8_t *kb_lds, const lds_u8_t *vb_lds) {
-    // ---- S^T = K . Q^T
+    // ---- S^T = K . Q^T - m (log2 units)
     f32x16_t sacc[2];
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb) {
       const int row = kb * 32 + rl;
-#pragma unroll
-      for (int e = 0; e < 16; ++e) sacc[kb][e] = 0.f;
 #pragma unroll
       for (int ks = 0; ks < KSTEPS; ++ks) {
         const int c = ks * 2 + half;
@@ -859,7 +951,8 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
             *(const __attribute__((address_space(3))) u32x4_t *)(kb_lds + row * ROWB +
                                                                   ((c ^ (row & 15)) << 4));
         sacc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, a),
-                                                           qf[ks], sacc[kb], 0, 0, 0);
+                                                           qf[ks], ks == 0 ? rm.negm : sacc[kb],
+                                                           0, 0, 0);
       }
     }
     // lane value e of block kb: key kt + kb*32 + (e/4)*8 + half*4 + e%4
@@ -874,39 +967,8 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
           sacc[kb][e] = ok ? sacc[kb][e] : -INFINITY;
         }
     }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[kb][e]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    // Lazy rescaling: the running max only moves when the tile's max
-    // exceeds it by more than 8 (log2 units), so probabilities stay below
-    // 2^8 and the accumulators are rescaled only on such tiles.
-    const bool bump = mx * scale2 > m_run + 8.0f;
-    if (__builtin_amdgcn_ballot_w64(bump)) {
-      const float m_new = bump ? mx * scale2 : m_run;
-      const float alpha = __builtin_amdgcn_exp2f(m_run - (m_new == -INFINITY ? 0.f : m_new));
-      m_run = m_new;
-      l_run *= alpha;
-#pragma unroll
-      for (int i = 0; i < DBLK; ++i)
-#pragma unroll
-        for (int e = 0; e < 16; ++e) acc_o[i][e] *= alpha;
-    }
-    const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
-    float psum = 0.f;
     uint32_t pk[2][8];
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int e = 0; e < 16; e += 2) {
-        const float p0 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][e], scale2, -m_use));
-        const float p1 = __builtin_amdgcn_exp2f(fmaf(sacc[kb][e + 1], scale2, -m_use));
-        psum += p0 + p1;
-        pk[kb][e >> 1] = pack2_bf16(p0, p1);
-      }
-    l_run += psum;
+    l_run = softmax_tile<DBLK>(sacc, rm, acc_o, l_run, pk);
 
     // ---- O^T += V^T . P^T
 #pragma unroll
@@ -969,8 +1031,8 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
     }
   }
 
-  finish_rows<D>(p, acc_o, m_run, l_run, row_ok, seq, h, hq, (int64_t)q_begin + pos_r, r, half,
-                 kr.n_sp, sp, p.v_deq ? p.v_deq[h] : 1.0f);
+  finish_rows<D>(p, acc_o, rm.final_max(), l_run, row_ok, seq, h, hq, (int64_t)q_begin + pos_r,
+                 r, half, kr.n_sp, sp, p.v_deq ? p.v_deq[h] : 1.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -1068,7 +1130,8 @@ int device_cus() {
 
 bool use_dma_kernel(const mia_prefill_args &a) {
   return a.head_dim == 128 && a.cache_dtype == MIA_DTYPE_BF16 && a.block_size % 16 == 0 &&
-         (64 % a.block_size == 0 || a.block_size % 64 == 0) && a.blocks_per_seq <= kDmaIds;
+         (64 % a.block_size == 0 || a.block_size % 64 == 0) && a.blocks_per_seq <= kDmaIds &&
+         a.k_cache_stride[0] == a.v_cache_stride[0] && a.k_cache_stride[2] == a.v_cache_stride[2];
 }
 
 }  // namespace
