@@ -450,7 +450,11 @@ MIA_DEV float softmax_tile(f32x16_t (&sacc)[2], RowMax &rm, f32x16_t (&acc_o)[DB
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
     for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sacc[kb][e]);
-  mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // the other k-group of the row
+  {  // the other k-group of the row: lanes l and l ^ 32 through one lane swap
+    const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                     false, false);
+    mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+  }
   const bool bump = rm.set ? (mx > 8.0f) : (mx > -INFINITY);
   if (__builtin_amdgcn_ballot_w64(bump)) {
     const float delta = bump ? mx : 0.f;
@@ -938,7 +942,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   const int tr_col = ((lane >> 4) & 1) * 16 + 4 * (tr_k & 3);
   const int tr_row = half * 4 + (tr_k >> 2);
 
-  auto compute_tile = [&](int kt, const lds_u8_t *kb_lds, const lds_u8_t *vb_lds) {
+  auto compute_tile = [&](int kt, const lds_u8_t *kb_lds, const lds_u8_t *vb_lds, auto &&after_qk) {
     // ---- S^T = K . Q^T - m (log2 units)
     f32x16_t sacc[2];
 #pragma unroll
@@ -955,6 +959,8 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
                                                            0, 0, 0);
       }
     }
+    // the copies of a later tile issue while these MFMAs execute
+    after_qk();
     // lane value e of block kb: key kt + kb*32 + (e/4)*8 + half*4 + e%4
     const bool full = (kt + kKT <= full_hi) && (kt >= full_lo);
     if (!full) {
@@ -1024,9 +1030,10 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
       __builtin_amdgcn_s_barrier();
       asm volatile("" ::: "memory");
       const int st_n = st == 0 ? STAGES - 1 : st - 1;  // (st + kAhead) % STAGES
-      if (kt + kAhead * kKT <= kt_last)
-        issue_tile(kt + kAhead * kKT, k_at(st_n), k_at(st_n) + TILEB);
-      compute_tile(kt, kv_base + st * 2 * TILEB, kv_base + st * 2 * TILEB + TILEB);
+      compute_tile(kt, kv_base + st * 2 * TILEB, kv_base + st * 2 * TILEB + TILEB, [&]() {
+        if (kt + kAhead * kKT <= kt_last)
+          issue_tile(kt + kAhead * kKT, k_at(st_n), k_at(st_n) + TILEB);
+      });
       st = st == STAGES - 1 ? 0 : st + 1;
     }
   }
