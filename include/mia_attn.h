@@ -319,7 +319,8 @@ typedef struct {
   int64_t out_stride[3]; /* token, hq, d */
   /* Split-K over keys: a long sequence's keys are cut into chunks of
    * split_tokens (a multiple of 64; 0 = chosen from the shapes) processed by
-   * separate workgroups, whose fp32 partials go to `workspace` and are
+   * separate workgroups, whose partials (bf16 o, fp32 max and sum) go to
+   * `workspace` and are
    * merged by a second kernel.  workspace_bytes must be at least
    * mia_prefill_workspace_bytes(args) (0 when no split is planned; then
    * workspace may be NULL). */

@@ -46,7 +46,9 @@ constexpr int kRowsW = 32;    // query rows per wave
 constexpr int kKT = 64;       // keys per tile
 constexpr int kKPad = 8;      // bf16 padding per K row in LDS
 constexpr int kVPad = 8;      // bf16 padding per V^T row in LDS
-constexpr int kPartPad = 4;   // a split partial row: o[D], m, l and 2 floats of padding
+// a split partial row: o[D] as bf16, then m and l (fp32) and 8 bytes of
+// padding (rows stay 16-byte aligned)
+constexpr int part_bytes(int D) { return 2 * D + 16; }
 constexpr int kMaxChunks = 8; // key chunks of a split row tile at most
 
 struct PrefillKParams {
@@ -73,7 +75,7 @@ struct PrefillKParams {
   uint16_t *out;
   int64_t os_t, os_h;
   // split-K over keys (nsplit == 1: off)
-  float *ws;      // [num_seqs, Hkv, rows_max, nsplit, D + 4] fp32 partials (o, m, l, pad)
+  uint8_t *ws;    // [num_seqs, Hkv, rows_max, nsplit] partial rows (part_bytes(D) each)
   int nsplit;     // chunks per row tile at most (grid z = nsplit * num_seqs)
   int num_seqs;
   int ksplit;     // keys per chunk (multiple of the 64-key tile)
@@ -369,21 +371,22 @@ MIA_DEV void finish_rows(const PrefillKParams &p, const f32x16_t (&acc_o)[D / 32
                          int r, int half, int n_sp, int sp, float vscale) {
   l_run += __shfl_xor(l_run, 32, 64);
   if (n_sp > 1) {
-    // split row tile: store this chunk's partial (o * vscale, m, l) for
-    // prefill_combine_kernel
+    // split row tile: store this chunk's partial (o * vscale as bf16, m,
+    // l) for prefill_combine_kernel; bf16 o halves the partial traffic and
+    // adds one bf16 rounding (relative 2^-9) to the merged output
     if (row_ok) {
-      float *w = p.ws + ((((int64_t)seq * p.Hkv + h) * p.rows_max + r) * p.nsplit + sp) *
-                            (int64_t)(D + kPartPad);
+      uint8_t *w = p.ws + ((((int64_t)seq * p.Hkv + h) * p.rows_max + r) * p.nsplit + sp) *
+                              (int64_t)part_bytes(D);
 #pragma unroll
       for (int db = 0; db < D / 32; ++db)
 #pragma unroll
         for (int e4 = 0; e4 < 4; ++e4) {
           const int d0 = db * 32 + e4 * 8 + half * 4;
-          *reinterpret_cast<f32x4_t *>(w + d0) =
-              f32x4_t{acc_o[db][e4 * 4] * vscale, acc_o[db][e4 * 4 + 1] * vscale,
-                      acc_o[db][e4 * 4 + 2] * vscale, acc_o[db][e4 * 4 + 3] * vscale};
+          *reinterpret_cast<u32x2_t *>(w + 2 * d0) =
+              u32x2_t{pack2_bf16(acc_o[db][e4 * 4] * vscale, acc_o[db][e4 * 4 + 1] * vscale),
+                      pack2_bf16(acc_o[db][e4 * 4 + 2] * vscale, acc_o[db][e4 * 4 + 3] * vscale)};
         }
-      if (half == 0) *reinterpret_cast<float2 *>(w + D) = make_float2(m_run, l_run);
+      if (half == 0) *reinterpret_cast<float2 *>(w + 2 * D) = make_float2(m_run, l_run);
     }
     return;
   }
@@ -1054,10 +1057,10 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
 template <int D>
 __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillKParams p) {
   constexpr int kRows = 64;          // rows per workgroup (4 waves x 16)
-  constexpr int LPR = D / 4;         // lanes per row
+  constexpr int LPR = D / 8;         // lanes per row (8 bf16 each)
   constexpr int RPS = 64 / LPR;      // rows per wave step
   constexpr int kSteps = 16 / RPS;
-  constexpr int PS = D + kPartPad;   // floats per partial row
+  constexpr int PB = part_bytes(D);  // bytes per partial row
   const int seq = blockIdx.z;
   const int h = blockIdx.y;
   const int q_begin = p.cu[seq];
@@ -1072,21 +1075,21 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillKParams p) 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
   const int sub = lane / LPR;
-  const int c4 = (lane % LPR) * 4;
+  const int c8 = (lane % LPR) * 8;
   const int64_t base = ((int64_t)seq * p.Hkv + h) * p.rows_max;
 #pragma unroll 2
   for (int step = 0; step < kSteps; ++step) {
     const int r = row0 + wave * 16 + step * RPS + sub;
     const bool ok = r < rows_total;
     const int rc = ok ? r : rows_total - 1;  // loads stay inside written rows
-    const float *w0 = p.ws + (base + rc) * p.nsplit * (int64_t)PS;
-    f32x4_t o[kMaxChunks];
+    const uint8_t *w0 = p.ws + (base + rc) * p.nsplit * (int64_t)PB;
+    u32x4_t o[kMaxChunks];
     float2 ml[kMaxChunks];
 #pragma unroll
     for (int j = 0; j < kMaxChunks; ++j) {
       if (j < n_sp) {
-        o[j] = *reinterpret_cast<const f32x4_t *>(w0 + j * PS + c4);
-        ml[j] = *reinterpret_cast<const float2 *>(w0 + j * PS + D);
+        o[j] = *reinterpret_cast<const u32x4_t *>(w0 + j * PB + 2 * c8);
+        ml[j] = *reinterpret_cast<const float2 *>(w0 + j * PB + 2 * D);
       }
     }
     const int pos_r = rc / p.G;
@@ -1098,21 +1101,27 @@ __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillKParams p) 
       if (j < n_sp) M = fmaxf(M, ml[j].x);
     const float Mu = (M == -INFINITY) ? 0.f : M;
     float L = __builtin_amdgcn_exp2f(sink2 - Mu);
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int j = 0; j < kMaxChunks; ++j) {
       if (j < n_sp) {
         const float f = __builtin_amdgcn_exp2f(ml[j].x - Mu);
         L += ml[j].y * f;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) acc[e] += o[j][e] * f;
+        for (int e = 0; e < 4; ++e) {
+          acc[2 * e] += __uint_as_float(o[j][e] << 16) * f;
+          acc[2 * e + 1] += __uint_as_float(o[j][e] & 0xffff0000u) * f;
+        }
       }
     }
     const float inv = L > 0.f ? 1.0f / L : 0.f;
     if (ok && q_begin + pos_r < p.num_tokens) {
-      uint16_t *op = p.out + (int64_t)(q_begin + pos_r) * p.os_t + (int64_t)hq * p.os_h + c4;
+      uint16_t *op = p.out + (int64_t)(q_begin + pos_r) * p.os_t + (int64_t)hq * p.os_h + c8;
+      // two 8-byte stores: the output is only 8-byte aligned
       *reinterpret_cast<u32x2_t *>(op) =
           u32x2_t{pack2_bf16(acc[0] * inv, acc[1] * inv), pack2_bf16(acc[2] * inv, acc[3] * inv)};
+      *reinterpret_cast<u32x2_t *>(op + 4) =
+          u32x2_t{pack2_bf16(acc[4] * inv, acc[5] * inv), pack2_bf16(acc[6] * inv, acc[7] * inv)};
     }
   }
 }
@@ -1184,7 +1193,7 @@ PrefillPlan plan_prefill(const mia_prefill_args &a) {
     pl.ws_bytes = 0;
   } else {
     pl.ws_bytes = (size_t)a.num_seqs * a.num_kv_heads * pl.rows_max * pl.nsplit *
-                                   (a.head_dim + kPartPad) * sizeof(float);
+                  part_bytes(a.head_dim);
   }
   return pl;
 }
@@ -1228,7 +1237,7 @@ int launch_paged_prefill(const mia_prefill_args &a, const PrefillPlan &pl, hipSt
   kp.out = (uint16_t *)a.out;
   kp.os_t = a.out_stride[0];
   kp.os_h = a.out_stride[1];
-  kp.ws = (float *)a.workspace;
+  kp.ws = (uint8_t *)a.workspace;
   kp.nsplit = pl.nsplit;
   kp.ksplit = pl.ksplit;
   kp.slots = pl.slots;
