@@ -1176,12 +1176,17 @@ PrefillPlan plan_prefill(const mia_prefill_args &a) {
   } else if (ks <= 0) {
     // Without the sequence lengths on the host, split only long tables
     // (>= 3072 keys) when the row tiles alone do not fill the device twice:
-    // chunks of a third of the table (rounded up to 512 keys), at least
-    // 1024 keys.
-    // A batch whose longest sequence is much longer than the others then
-    // spreads the long one over more workgroups.
+    // chunks of half the table (rounded up to 512 keys), at least 1024
+    // keys.  A batch whose longest sequence is much longer than the others
+    // then spreads the long one over more workgroups.  Halves rather than
+    // thirds or quarters: each chunk pays the workgroup's fixed start-up
+    // and its partial traffic (4 x 512 on priors U[0, 4096]: 73.5 us in
+    // halves, 79.9 in thirds, 95.9 in quarters; 2 x 512 on 8k priors 149 /
+    // 179 / 172 us; 1 x 1024 on a 16k prior 269 / 322 / 288 us; short
+    // chunks of many uneven sequences prefer quarters: 4 x 256 on priors
+    // U[0, 8192] 89 / 69 / 60 us).
     ks = (s_ctx >= 3072 && base_wgs < 2 * (int64_t)slots)
-             ? std::max<int64_t>(1024, ((s_ctx + 2) / 3 + 511) / 512 * 512)
+             ? std::max<int64_t>(1024, ((s_ctx + 1) / 2 + 511) / 512 * 512)
              : (int64_t)1 << 30;
   }
   ks = std::max<int64_t>(ks, (s_ctx + kMaxChunks - 1) / kMaxChunks);  // merged in registers
