@@ -333,8 +333,8 @@ MIA_DEV uint3 ranked_tile(const PrefillKParams &p, int *scratch, int cap, SeqInf
 // d = db*32 + (e/4)*8 + half*4 + e%4 of its row (lane % 32); m_run / l_run
 // are the row's running max (log2 domain) and this lane's partial sum.
 // Unsplit rows are normalised (sink in the denominator only, rows with no
-// visible key -> 0) and stored as bf16; split rows store the fp32 partial
-// (o * vscale, m, l) of chunk sp for prefill_combine_kernel.
+// visible key -> 0) and stored as bf16; split rows store the partial
+// (o * vscale as bf16, m, l as fp32) of chunk sp for prefill_combine_kernel.
 // Normalises one row (sink in the denominator only; a row with no visible
 // key gives 0) and stores it as bf16.  l_run is the row's full sum.
 template <int D>
@@ -747,8 +747,9 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
 // rows) per workgroup and the 64-key K and V tiles travelling HBM -> LDS
 // with global_load_lds_dwordx4 (no registers, no VALU) through a 3-stage
 // ring: tiles t+1 and t+2 are in flight while tile t is computed, one
-// barrier per tile.  The block ids of the workgroup's key range are staged
-// in LDS once, so no global load sits between two tiles' copies.
+// barrier per tile.  The byte offsets of the blocks of the workgroup's key
+// range are staged in LDS once, so no global load sits between two tiles'
+// copies.
 // A DMA instruction writes 64 lanes x 16 B contiguously, i.e. 4 rows of
 // 256 B; each lane picks which 16-byte chunk of its row it fetches, which
 // stores the rows XOR-swizzled:
@@ -803,7 +804,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   // heaviest work item first (the block-id buffer is free until it is filled)
   SeqInfo si;
   const uint3 tile = ranked_tile(p, reinterpret_cast<int *>(offs_lds), 2 * kDmaIds, si);
-  __syncthreads();  // the ranking scratch is read before the block ids land
+  __syncthreads();  // the ranking scratch is read before the block offsets land
   const int sp = tile.z / p.num_seqs;  // key chunk of a split row tile
   const int seq = tile.z - sp * p.num_seqs;
   const int h = tile.y;
@@ -845,7 +846,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   // Q pre-multiplied by the softmax scale (log2 units) and rounded to bf16,
   // so that the MFMA yields scaled scores and the softmax needs no multiply
   const float scale2 = p.scale_log2 * (p.k_deq ? p.k_deq[h] : 1.0f);
-  u32x4_t qw[KSTEPS];  // raw bf16 Q, scaled once the block ids are staged
+  u32x4_t qw[KSTEPS];  // raw bf16 Q, scaled once the block offsets are staged
   {
     const uint16_t *qp = p.q + (int64_t)(q_begin + (row_ok ? pos_r : 0)) * p.qs_t +
                          (int64_t)(row_ok ? hq : 0) * p.qs_h;
@@ -857,7 +858,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   }
   const int64_t bt_row = (int64_t)seq * p.bt_s + (int64_t)h * p.bt_h;
 
-  // ---- block ids of blocks b_lo .. b_hi (clamped into the pool)
+  // ---- byte offsets of blocks b_lo .. b_hi (ids clamped into the pool)
   const int b_lo = (int)fdiv((uint32_t)kt0, p.bs_div);
   const int b_hi = min((int)fdiv((uint32_t)(kt_last + kKT - 1), p.bs_div), p.nblk - 1);
   if (any_key) {
@@ -1049,11 +1050,11 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
 // split-K merge
 // ---------------------------------------------------------------------------
 // 64 rows per workgroup (rows of unsplit row tiles exit at once).  A row's
-// partial of one chunk is D fp32 (16-byte aligned rows of D + 4 floats), so
-// D/4 lanes cover it with one 16-byte load each and a wave steps over
-// 64/(D/4) rows at a time; all chunks' loads of a step are issued together.
-// The n_sp partials (o, m, l; log2 domain) are merged in chunk order, the
-// sink joins the denominator and the bf16 row is stored (8 bytes per lane).
+// partial of one chunk holds o as D bf16 (then m and l), so D/8 lanes cover
+// it with one 16-byte load each and a wave steps over 64/(D/8) rows at a
+// time; all chunks' loads of a step are issued together.  The n_sp partials
+// (o, m, l; log2 domain) are merged in fp32 in chunk order, the sink joins
+// the denominator and the bf16 row is stored (16 bytes per lane).
 template <int D>
 __global__ __launch_bounds__(256) void prefill_combine_kernel(PrefillKParams p) {
   constexpr int kRows = 64;          // rows per workgroup (4 waves x 16)
