@@ -229,3 +229,36 @@ def test_split_keys_match_unsplit_and_reference(gpu, case, split):
                              None if sink is None else sink.cpu())
         err = (out[s0:s1].float().cpu().double() - f).abs().max().item()
         assert err <= tol, (i, err)
+
+
+def test_copy_ring_and_register_kernels_agree(gpu):
+    """A bf16 d = 128 cache runs the copy-ring kernel, whose copies share the
+    block offsets of K and V; a V cache with its own block stride (a view of
+    a wider allocation) takes the register-staged kernel.  Both match float64
+    math, and each other to within two bf16 steps."""
+    priors = [700, 96]
+    cfg = W.PrefillConfig("r", len(priors), 16, 4, 128, 32, 160, max(priors), max(priors),
+                          seed=131)
+    b = W.make_prefill_batch(cfg, gpu)
+    K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache)
+    nb, Hkv, bs, d = b.v_cache.shape
+    wide = torch.zeros(nb, Hkv + 1, bs, d, dtype=b.v_cache.dtype, device=gpu)
+    wide[:, :Hkv].copy_(b.v_cache)
+    v_view = wide[:, :Hkv]
+    assert v_view.stride(0) != b.k_cache.stride(0)
+    prior = torch.tensor(priors, dtype=torch.int32, device=gpu)
+    scale = d ** -0.5
+    ring = K.paged_prefill(b.q, b.cu_seqlens, prior, cfg.new_tokens, b.k_cache, b.v_cache,
+                           b.block_table, scale=scale)
+    regs = K.paged_prefill(b.q, b.cu_seqlens, prior, cfg.new_tokens, b.k_cache, v_view,
+                           b.block_table, scale=scale)
+    assert (ring.float() - regs.float()).abs().max().item() <= 1.6e-2
+    for i, pr in enumerate(priors):
+        s0, s1 = int(b.cu_seqlens[i]), int(b.cu_seqlens[i + 1])
+        n = pr + (s1 - s0)
+        ks = _seq_kv(b.k_cache.cpu(), b.block_table[i].cpu(), n, Hkv)
+        vs = _seq_kv(b.v_cache.cpu(), b.block_table[i].cpu(), n, Hkv)
+        f = OSg.fp32_prefill(b.q[s0:s1].cpu(), ks, vs, pr, scale, 0, None)
+        for out in (ring, regs):
+            err = (out[s0:s1].float().cpu().double() - f).abs().max().item()
+            assert err <= TOL_BF16, (i, err)
