@@ -3,7 +3,7 @@
 //
 // Work decomposition (split kernel)
 //   The attended prior tiles (32 tokens) of every (batch row b, kv head h)
-//   segment are laid end to end; the grid is persistent (2 or 3 workgroups
+//   segment are laid end to end; the grid is persistent (1 or 2 workgroups
 //   of 4 waves per CU) and streaming wave w takes a contiguous share of the
 //   tiles (weighted by dispatch class: earlier workgroups on a CU issue
 //   first and stream faster), keeping one online-softmax state per segment piece, so
@@ -59,12 +59,20 @@ namespace mia {
 namespace {
 
 constexpr int kWaves = 4;
-// resident workgroups per CU of the persistent grid: 2 (8 waves, 256 VGPRs
-// each).  With streaming V loads an FP8 cache no longer needs a third
-// workgroup to keep HBM busy, and at 2 the FP8 kernels do not spill (at 3
-// they were capped at 168 VGPRs and spilled 28-76 bytes per lane): the
-// B=16 32k-token FP8 decode measured 167 us at 3, 150 us at 2.
+// occupancy the split kernel is compiled for: 2 workgroups per CU (8 waves,
+// 256 VGPRs each).  With streaming V loads an FP8 cache no longer needs a
+// third workgroup to keep HBM busy, and at 2 the FP8 kernels do not spill
+// (at 3 they were capped at 168 VGPRs and spilled 28-76 bytes per lane):
+// the B=16 32k-token FP8 decode measured 167 us at 3, 150 us at 2.
 constexpr int wg_per_cu(int D, bool fp8) { return (void)D, (void)fp8, 2; }
+// workgroups per CU the persistent grid launches.  A bf16 d = 128 tile
+// keeps 16 KB per wave in flight, and one workgroup per CU (16 MB in flight
+// over the device) already saturates HBM: it streams the
+// Llama-3-8B decode faster than two (split 179.6 against 184.2 us, with
+// fewer segment pieces for the combine), while the d = 64 and FP8 tiles
+// (8 KB per wave) need the second workgroup (GPT-OSS full layer 117.2
+// against 98.4 us at one, B=16 32k FP8 220.6 against 145.5 us).
+constexpr int grid_wg_per_cu(int D, bool fp8) { return (D == 128 && !fp8) ? 1 : 2; }
 constexpr int kTile = 32;  // tokens per wave tile
 constexpr int kPMax = 128;
 constexpr int kMaxMinTiles = 8;        // longest minimum tile range of a streaming wave
@@ -999,7 +1007,7 @@ DecodePlan plan_decode(const mia_decode_args &a) {
   // down to single tiles, so that the work still spreads.  A segment of at
   // most t_max tiles then meets at most ceil(t_max / min_tiles) + 1 waves:
   // its partial slots.
-  const int wgs_cu = wg_per_cu(a.head_dim, a.cache_dtype == MIA_DTYPE_FP8_E4M3FN);
+  const int wgs_cu = grid_wg_per_cu(a.head_dim, a.cache_dtype == MIA_DTYPE_FP8_E4M3FN);
   const int64_t waves = wgs_cu * (int64_t)device_cu_count() * kWaves;
   const int t_max = (s_ctx + kTile - 1) / kTile;
   const int64_t n_max = (int64_t)a.batch * a.num_kv_heads * t_max;
@@ -1013,7 +1021,7 @@ DecodePlan plan_decode(const mia_decode_args &a) {
   pl.num_splits = t_max > 0 ? (t_max + mt - 1) / mt + 1 : 1;
   pl.ncols = G * a.s_active;
   pl.col_groups = (pl.ncols + 15) / 16;
-  // persistent grid: wg_per_cu workgroups of four streaming waves per CU,
+  // persistent grid: grid_wg_per_cu workgroups of four streaming waves per CU,
   // or fewer when fewer waves can have min_tiles tiles each
   const int64_t wg = (std::max<int64_t>(1, n_max / mt) + kWaves - 1) / kWaves;
   const int64_t cap = wgs_cu * (int64_t)device_cu_count();
