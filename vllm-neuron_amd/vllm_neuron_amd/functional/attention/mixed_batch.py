@@ -16,7 +16,11 @@ The two launches run back to back: the decode is HBM-bound and needs every
 CU to approach the memory roofline (at the Llama-3-8B mixed shape its 60
 rows take 525 / 299 / 203 us on 64 / 128 / 256 CUs), and the two kernels
 run concurrently on complementary CU-masked streams measured 445-510 us
-against 295 us back to back, so the GPU is not split between them.
+against 295 us back to back, so the GPU is not split between them.  Two
+unmasked streams, with the decode at one or two workgroups per CU and the
+prefill on its copy-ring or its register-staged kernel (which fit beside a
+decode workgroup on a CU), took 320-372 us against 267-293 us back to
+back: the kernels slow each other down more than they overlap.
 """
 from __future__ import annotations
 
