@@ -124,6 +124,11 @@ def _prefill_args(**over):
     (dict(k_packed=1, cache_dtype=N.DTYPE_FP8_E4M3FN), "pairs contiguous"),
     (dict(k_packed=1, cache_dtype=N.DTYPE_FP8_E4M3FN,
           k_cache_stride=(ctypes.c_int64 * 5)(16384, 8192, 264, 2, 1)), "pairs contiguous"),
+    # the kernels hold strides as 32-bit element counts
+    (dict(q_stride=(ctypes.c_int64 * 3)(1 << 31, 128, 1)), r"strides must be in \[0, 2\^31\)"),
+    (dict(k_cache_stride=(ctypes.c_int64 * 5)(1 << 31, 8192, 128, 1, 0),
+          v_cache_stride=(ctypes.c_int64 * 4)(1 << 31, 8192, 128, 1)), r"strides must be in"),
+    (dict(bt_stride=(ctypes.c_int64 * 3)(-2, 0, 1)), r"strides must be in"),
 ])
 def test_prefill_bounds_validation(over, text):
     a = _prefill_args(**over)

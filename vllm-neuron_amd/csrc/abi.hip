@@ -293,6 +293,18 @@ static int validate_prefill(const mia_prefill_args *a) {
               "prefill: bound_min and bound_max must both be set or both be NULL");
   MIA_REQUIRE(a->bound_stride[0] >= 0 && a->bound_stride[1] >= 0, MIA_ERR_VALUE,
               "prefill: negative bound strides");
+  {
+    // the kernels hold the strides as 32-bit element counts
+    const int64_t lim = (int64_t)1 << 31;
+    bool ok = true;
+    for (int i = 0; i < 3; ++i) ok = ok && a->q_stride[i] >= 0 && a->q_stride[i] < lim;
+    for (int i = 0; i < 3; ++i) ok = ok && a->k_cache_stride[i] >= 0 && a->k_cache_stride[i] < lim;
+    for (int i = 0; i < 3; ++i) ok = ok && a->v_cache_stride[i] >= 0 && a->v_cache_stride[i] < lim;
+    for (int i = 0; i < 3; ++i) ok = ok && a->bt_stride[i] >= 0 && a->bt_stride[i] < lim;
+    for (int i = 0; i < 3; ++i) ok = ok && a->out_stride[i] >= 0 && a->out_stride[i] < lim;
+    for (int i = 0; i < 2; ++i) ok = ok && a->bound_stride[i] < lim;
+    MIA_REQUIRE(ok, MIA_ERR_VALUE, "prefill: strides must be in [0, 2^31) elements");
+  }
   return MIA_OK;
 }
 

@@ -333,7 +333,7 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
 
   // ---- setup (every workgroup): prior range of each row and the prefix
   // sum R of its tiles over the kv heads
-  for (int r = threadIdx.x; r < p.B; r += blockDim.x) {
+  for (int r = threadIdx.x; r < p.B; r += kWaves * 64) {
     const RowInfo ri = row_info(p.pos, p.start, p.mask_mode, p.S, p.s_ctx, r);
     s_lo[r] = ri.lo;
     s_hi[r] = ri.hi;
@@ -364,7 +364,7 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
                  (int)((int64_t)n_tiles * p.cls_w[2] /
                        ((int64_t)p.cls_w[0] * (p.min_tiles + 1)))));
   if (blockIdx.x == 0) {  // the combine kernel re-derives the slots from these
-    for (int r = threadIdx.x; r <= p.B; r += blockDim.x) p.ws_hdr[r] = s_R[r];
+    for (int r = threadIdx.x; r <= p.B; r += kWaves * 64) p.ws_hdr[r] = s_R[r];
     if (threadIdx.x == 0) p.ws_hdr[p.B + 1] = n_waves;
   }
   const int w_id = readfirstlane(blockIdx.x * kWaves + wave);

@@ -53,15 +53,15 @@ constexpr int kMaxChunks = 8; // key chunks of a split row tile at most
 
 struct PrefillKParams {
   const uint16_t *q;
-  int64_t qs_t, qs_h;
+  int32_t qs_t, qs_h;  // strides in elements (below 2^31: checked by the host)
   const int32_t *cu;
   const int32_t *prior;
   const uint8_t *k_cache;
   const uint8_t *v_cache;
-  int64_t kc_blk, kc_h, kc_t;
-  int64_t vc_blk, vc_h, vc_t;
+  int32_t kc_blk, kc_h, kc_t;
+  int32_t vc_blk, vc_h, vc_t;
   const int32_t *bt;
-  int64_t bt_s, bt_h, bt_j;
+  int32_t bt_s, bt_h, bt_j;
   int nblk, bs, nb;
   FastDiv bs_div;
   int Hq, Hkv, G;
@@ -73,7 +73,7 @@ struct PrefillKParams {
   int fp8;
   int num_tokens;
   uint16_t *out;
-  int64_t os_t, os_h;
+  int32_t os_t, os_h;
   // split-K over keys (nsplit == 1: off)
   uint8_t *ws;    // [num_seqs, Hkv, rows_max, nsplit] partial rows (part_bytes(D) each)
   int nsplit;     // chunks per row tile at most (grid z = nsplit * num_seqs)
@@ -85,7 +85,7 @@ struct PrefillKParams {
   // generalised visibility (dense attention); all zero = segmented rule
   const int32_t *kv_len;          // [num_seqs] keys per sequence (NULL: prior + S_q)
   const int32_t *bmin, *bmax;     // per (token, q head) key bounds or NULL
-  int64_t b_st, b_sh;
+  int32_t b_st, b_sh;
   int non_causal;                 // every existing key visible
   int q_off;                      // added to query positions
   int uniform;                    // empty rows (no sink) attend uniformly
@@ -270,10 +270,12 @@ constexpr uint32_t kRankMax = 512;  // items per XCD ranked at most
 // its start (the cost inputs are global loads), so it is used for batches
 // of several sequences only.  For one sequence the row tiles already go
 // heaviest first (xcd_tile).
-// Every thread of the workgroup must call this (two barriers); `scratch`
-// holds cap ints of 16-byte aligned LDS.  Falls back to xcd_tile when the
-// host did not ask for ranking, the group count is not a multiple of 8 or
-// an XCD has more items than the scratch or kRankMax.
+// Every thread of the workgroup (NT threads) must call this (two barriers);
+// `scratch` holds cap ints of 16-byte aligned LDS.  Falls back to xcd_tile
+// when the host did not ask for ranking, the group count is not a multiple
+// of 8 or an XCD has more items than the scratch, NT or kRankMax.  NT is a
+// template argument: blockDim.x would be a load from the dispatch arguments.
+template <uint32_t NT>
 MIA_DEV uint3 ranked_tile(const PrefillKParams &p, int *scratch, int cap, SeqInfo &info) {
   constexpr uint32_t X = 8;
   const uint32_t R = gridDim.x;
@@ -282,7 +284,7 @@ MIA_DEV uint3 ranked_tile(const PrefillKParams &p, int *scratch, int cap, SeqInf
   // LDS: costs [0, n_x), the chosen item at [n_x], item metadata from mo
   const uint32_t mo = (n_x + 4) & ~3u;
   if (!p.rank_items || groups % X != 0 || mo + 4 * n_x > (uint32_t)cap || n_x > kRankMax ||
-      n_x > blockDim.x) {
+      n_x > NT) {
     const uint3 t = xcd_tile();
     info = load_seq(p, (int)(t.z % (uint32_t)p.num_seqs));
     return t;
@@ -302,7 +304,7 @@ MIA_DEV uint3 ranked_tile(const PrefillKParams &p, int *scratch, int cap, SeqInf
   __syncthreads();
   // rank of item j: items of higher cost, or of equal cost and lower index,
   // counted 64 at a time with a ballot; each wave ranks every nw-th item
-  const uint32_t lane = tid & 63, wv = tid >> 6, nw = blockDim.x >> 6;
+  const uint32_t lane = tid & 63, wv = tid >> 6, nw = NT >> 6;
   for (uint32_t j = wv; j < n_x; j += nw) {
     const int cj = scratch[j];
     uint32_t rank = 0;
@@ -315,11 +317,12 @@ MIA_DEV uint3 ranked_tile(const PrefillKParams &p, int *scratch, int cap, SeqInf
     if (rank == k && lane == 0) scratch[n_x] = (int)j;
   }
   __syncthreads();
-  const uint32_t jj = (uint32_t)scratch[n_x];
+  // LDS values are wave-uniform: kept in scalar registers
+  const uint32_t jj = (uint32_t)readfirstlane(scratch[n_x]);
   const i32x4_t w = *reinterpret_cast<const i32x4_t *>(scratch + mo + 4 * jj);
-  info.q_begin = w[0];
-  info.S_q = w[1];
-  info.prior = w[2];
+  info.q_begin = readfirstlane(w[0]);
+  info.S_q = readfirstlane(w[1]);
+  info.prior = readfirstlane(w[2]);
   info.pad = 0;
   const uint32_t g = x + X * (jj / R);
   uint3 t;
@@ -513,7 +516,7 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
 
   // heaviest work item first (the K tile buffer is free until the loop)
   SeqInfo si;
-  const uint3 tile = ranked_tile(p, reinterpret_cast<int *>(k_lds), (int)(sizeof(k_lds) / 4), si);
+  const uint3 tile = ranked_tile<256>(p, reinterpret_cast<int *>(k_lds), (int)(sizeof(k_lds) / 4), si);
   __syncthreads();  // the ranking scratch is read before the first K tile store
   const int sp = tile.z / p.num_seqs;  // key chunk of a split row tile
   const int seq = tile.z - sp * p.num_seqs;
@@ -803,7 +806,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
 
   // heaviest work item first (the block-id buffer is free until it is filled)
   SeqInfo si;
-  const uint3 tile = ranked_tile(p, reinterpret_cast<int *>(offs_lds), 2 * kDmaIds, si);
+  const uint3 tile = ranked_tile<WAVES * 64>(p, reinterpret_cast<int *>(offs_lds), 2 * kDmaIds, si);
   __syncthreads();  // the ranking scratch is read before the block offsets land
   const int sp = tile.z / p.num_seqs;  // key chunk of a split row tile
   const int seq = tile.z - sp * p.num_seqs;
@@ -862,7 +865,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   const int b_lo = (int)fdiv((uint32_t)kt0, p.bs_div);
   const int b_hi = min((int)fdiv((uint32_t)(kt_last + kKT - 1), p.bs_div), p.nblk - 1);
   if (any_key) {
-    for (int i = tid; i <= b_hi - b_lo; i += blockDim.x) {
+    for (int i = tid; i <= b_hi - b_lo; i += WAVES * 64) {
       int32_t v = p.bt[bt_row + (int64_t)(b_lo + i) * p.bt_j];
       v = v < 0 ? 0 : (v >= p.nb ? p.nb - 1 : v);
       offs_lds[i] = (int64_t)v * p.kc_blk * 2;
@@ -1209,23 +1212,23 @@ int launch_paged_prefill(const mia_prefill_args &a, const PrefillPlan &pl, hipSt
   const bool fp8 = a.cache_dtype == MIA_DTYPE_FP8_E4M3FN;
   PrefillKParams kp;
   kp.q = (const uint16_t *)a.q;
-  kp.qs_t = a.q_stride[0];
-  kp.qs_h = a.q_stride[1];
+  kp.qs_t = (int32_t)a.q_stride[0];
+  kp.qs_h = (int32_t)a.q_stride[1];
   kp.cu = a.cu_seqlens_q;
   kp.prior = a.prior_tokens;
   kp.k_cache = (const uint8_t *)a.k_cache;
   kp.v_cache = (const uint8_t *)a.v_cache;
-  kp.kc_blk = a.k_cache_stride[0];
-  kp.kc_h = a.k_cache_stride[1];
+  kp.kc_blk = (int32_t)a.k_cache_stride[0];
+  kp.kc_h = (int32_t)a.k_cache_stride[1];
   // packed K: the token stride of the even token of a pair
-  kp.kc_t = a.k_packed ? a.k_cache_stride[2] / 2 : a.k_cache_stride[2];
-  kp.vc_blk = a.v_cache_stride[0];
-  kp.vc_h = a.v_cache_stride[1];
-  kp.vc_t = a.v_cache_stride[2];
+  kp.kc_t = (int32_t)(a.k_packed ? a.k_cache_stride[2] / 2 : a.k_cache_stride[2]);
+  kp.vc_blk = (int32_t)a.v_cache_stride[0];
+  kp.vc_h = (int32_t)a.v_cache_stride[1];
+  kp.vc_t = (int32_t)a.v_cache_stride[2];
   kp.bt = a.block_table;
-  kp.bt_s = a.bt_stride[0];
-  kp.bt_h = a.bt_stride[1];
-  kp.bt_j = a.bt_stride[2];
+  kp.bt_s = (int32_t)a.bt_stride[0];
+  kp.bt_h = (int32_t)a.bt_stride[1];
+  kp.bt_j = (int32_t)a.bt_stride[2];
   kp.nblk = a.blocks_per_seq;
   kp.bs = a.block_size;
   kp.nb = a.num_blocks;
@@ -1241,8 +1244,8 @@ int launch_paged_prefill(const mia_prefill_args &a, const PrefillPlan &pl, hipSt
   kp.fp8 = fp8 ? 1 : 0;
   kp.num_tokens = a.num_tokens;
   kp.out = (uint16_t *)a.out;
-  kp.os_t = a.out_stride[0];
-  kp.os_h = a.out_stride[1];
+  kp.os_t = (int32_t)a.out_stride[0];
+  kp.os_h = (int32_t)a.out_stride[1];
   kp.ws = (uint8_t *)a.workspace;
   kp.nsplit = pl.nsplit;
   kp.ksplit = pl.ksplit;
@@ -1253,8 +1256,8 @@ int launch_paged_prefill(const mia_prefill_args &a, const PrefillPlan &pl, hipSt
   kp.kv_len = a.kv_len;
   kp.bmin = a.bound_min;
   kp.bmax = a.bound_max;
-  kp.b_st = a.bound_stride[0];
-  kp.b_sh = a.bound_stride[1];
+  kp.b_st = (int32_t)a.bound_stride[0];
+  kp.b_sh = (int32_t)a.bound_stride[1];
   kp.non_causal = a.non_causal ? 1 : 0;
   kp.q_off = a.q_offset;
   kp.uniform = a.empty_rows_uniform ? 1 : 0;
