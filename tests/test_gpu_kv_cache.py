@@ -93,6 +93,36 @@ def test_kv_write_fp8_bit_exact(gpu, mode, per_head):
     assert torch.equal(_bytes(vcd), _bytes(vc))
 
 
+@pytest.mark.parametrize("fp8", [False, True])
+def test_kv_write_vector_and_element_paths_agree(gpu, fp8):
+    """Contiguous bf16 rows take the 8-element vector kernel; the same values
+    as a strided view (head_dim stride 2) take the per-element kernel: the
+    caches must end up byte-identical, K-only writes included."""
+    g = torch.Generator().manual_seed(3)
+    nb, H, bs, d, T = 24, 8, 32, 128, 200
+    k = (torch.randn((T, H, d), generator=g) * 20).to(torch.bfloat16)
+    v = (torch.randn((T, H, d), generator=g) * 20).to(torch.bfloat16)
+    wide = torch.zeros((2, T, H, 2 * d), dtype=torch.bfloat16)
+    wide[0, ..., ::2] = k
+    wide[1, ..., ::2] = v
+    slots = torch.randperm(nb * bs, generator=g)[:T]
+    slots[5] = -1
+    kw = {}
+    if fp8:
+        kw = dict(quant_mode=N.QUANT_MUL_F32, k_scale=torch.tensor([0.6, 1.2, 0.9, 1.0, 0.7, 1.1, 0.8, 1.3]).to(gpu),
+                  v_scale=torch.tensor([1.1, 0.6, 1.0, 0.9, 1.2, 0.8, 0.7, 1.3]).to(gpu), scale_per_head=True)
+    dt = torch.float8_e4m3fn if fp8 else torch.bfloat16
+    caches = [torch.zeros((nb, H, bs, d), dtype=dt, device=gpu) for _ in range(6)]
+    kd, vd, wd = k.to(gpu), v.to(gpu), wide.to(gpu)
+    assert wd[0, ..., ::2].stride(-1) == 2
+    K.kv_write(kd, vd, slots.to(gpu), caches[0], caches[1], **kw)                            # vector
+    K.kv_write(wd[0, ..., ::2], wd[1, ..., ::2], slots.to(gpu), caches[2], caches[3], **kw)  # element
+    K.kv_write(kd, None, slots.to(gpu), caches[4], None, **kw)                             # K only
+    assert torch.equal(_bytes(caches[0]), _bytes(caches[2]))
+    assert torch.equal(_bytes(caches[1]), _bytes(caches[3]))
+    assert torch.equal(_bytes(caches[4]), _bytes(caches[0]))
+
+
 def test_kv_write_packed_k(gpu):
     g = torch.Generator().manual_seed(2)
     nb, H, bs, d, T = 10, 2, 16, 64, 21

@@ -99,6 +99,63 @@ __global__ void kv_write_kernel(mia_kv_write_args a) {
   }
 }
 
+// Vector form of kv_write for bf16 sources with contiguous head_dim and a
+// bf16 or (unpacked) FP8 cache with contiguous head_dim: one thread per
+// 8-element chunk of a row (16-byte source loads; 16-byte bf16 or 8-byte
+// FP8 stores), K and V.  Same element values as kv_write_kernel (the FP8
+// codes come from the same quantize / cast per element).
+template <bool FP8>
+__global__ __launch_bounds__(256) void kv_write_vec_kernel(mia_kv_write_args a, int64_t chunks) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= chunks) return;
+  const int cpr = a.head_dim >> 3;  // chunks per row
+  const int64_t row = i / cpr;      // token * Hkv + head
+  const int c8 = (int)(i - row * cpr) * 8;
+  const int64_t t = row / a.num_kv_heads;
+  const int h = (int)(row - t * a.num_kv_heads);
+  const int64_t max_slot = (int64_t)a.num_blocks * a.block_size;
+  const int64_t slot = load_slot(a.slots, t, a.slot_dtype);
+  if (slot < 0 || slot >= max_slot) return;  // sentinel: skipped
+  const int64_t blk = slot / a.block_size;
+  const int64_t off = slot - blk * a.block_size;
+  const int64_t kdst = blk * a.k_cache_stride[0] + h * a.k_cache_stride[1] +
+                       off * a.k_cache_stride[2] + c8;
+  const int64_t vdst = blk * a.v_cache_stride[0] + h * a.v_cache_stride[1] +
+                       off * a.v_cache_stride[2] + c8;
+  const int64_t ksrc = t * a.k_src_stride[0] + h * a.k_src_stride[1] + c8;
+  const int64_t vsrc = t * a.v_src_stride[0] + h * a.v_src_stride[1] + c8;
+  const u32x4_t kw = *reinterpret_cast<const u32x4_t *>((const uint16_t *)a.k_src + ksrc);
+  u32x4_t vw = {0u, 0u, 0u, 0u};
+  if (a.v_src) vw = *reinterpret_cast<const u32x4_t *>((const uint16_t *)a.v_src + vsrc);
+  if constexpr (!FP8) {
+    *reinterpret_cast<u32x4_t *>((uint16_t *)a.k_cache + kdst) = kw;
+    if (a.v_src) *reinterpret_cast<u32x4_t *>((uint16_t *)a.v_cache + vdst) = vw;
+  } else {
+    float ks = 1.0f, vs = 1.0f;
+    if (a.quant_mode != MIA_QUANT_NONE) {
+      ks = a.k_scale[a.scale_per_head ? h : 0];
+      if (a.v_scale) vs = a.v_scale[a.scale_per_head ? h : 0];
+    }
+    auto code = [&](uint32_t bits, float s) -> uint32_t {
+      const float x = bf16_bits_to_f32(bits);
+      return a.quant_mode == MIA_QUANT_NONE ? f32_to_e4m3fn_bits(x)
+                                            : quantize_e4m3fn(x, s, a.quant_mode);
+    };
+    auto pack = [&](u32x4_t w, float s) -> u32x2_t {
+      u32x2_t o;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const uint32_t lo = w[2 * q], hi = w[2 * q + 1];
+        o[q] = code(lo & 0xffffu, s) | (code(lo >> 16, s) << 8) | (code(hi & 0xffffu, s) << 16) |
+               (code(hi >> 16, s) << 24);
+      }
+      return o;
+    };
+    *reinterpret_cast<u32x2_t *>((uint8_t *)a.k_cache + kdst) = pack(kw, ks);
+    if (a.v_src) *reinterpret_cast<u32x2_t *>((uint8_t *)a.v_cache + vdst) = pack(vw, vs);
+  }
+}
+
 MIA_DEV int elem_bytes(int dtype) {
   return dtype == MIA_DTYPE_FP8_E4M3FN ? 1 : (dtype == MIA_DTYPE_F32 ? 4 : 2);
 }
@@ -381,9 +438,40 @@ inline unsigned grid_for(int64_t n, int threads) {
 
 }  // namespace
 
+// The vector kernel's layout conditions: bf16 source rows and cache rows
+// with contiguous head_dim, 16-byte aligned source chunks, 16-byte (bf16)
+// or 8-byte (FP8) aligned cache chunks, unpacked K.
+static bool kv_write_vec_ok(const mia_kv_write_args &a) {
+  const bool fp8 = a.cache_dtype == MIA_DTYPE_FP8_E4M3FN;
+  if (a.src_dtype != MIA_DTYPE_BF16 || a.head_dim % 8 != 0 || a.k_packed) return false;
+  if (a.cache_dtype != MIA_DTYPE_BF16 && !fp8) return false;
+  const int eb = fp8 ? 1 : 2, al = 8 * eb;  // cache chunk bytes
+  auto src_ok = [&](const void *p, const int64_t *st) {
+    return p == nullptr ||
+           (st[2] == 1 && (uintptr_t)p % 16 == 0 && (st[0] * 2) % 16 == 0 && (st[1] * 2) % 16 == 0);
+  };
+  auto cache_ok = [&](const void *p, const int64_t *st) {
+    return st[3] == 1 && (uintptr_t)p % al == 0 && (st[0] * eb) % al == 0 &&
+           (st[1] * eb) % al == 0 && (st[2] * eb) % al == 0;
+  };
+  return src_ok(a.k_src, a.k_src_stride) && src_ok(a.v_src, a.v_src_stride) &&
+         cache_ok(a.k_cache, a.k_cache_stride) &&
+         (a.v_src == nullptr || cache_ok(a.v_cache, a.v_cache_stride));
+}
+
 int launch_kv_write(const mia_kv_write_args &a, hipStream_t s) {
   const int64_t rows = a.num_tokens * a.num_kv_heads;
   if (rows == 0) return MIA_OK;
+  if (kv_write_vec_ok(a)) {
+    const int64_t chunks = rows * (a.head_dim / 8);
+    if (a.cache_dtype == MIA_DTYPE_FP8_E4M3FN)
+      hipLaunchKernelGGL(kv_write_vec_kernel<true>, dim3(grid_for(chunks, 256)), dim3(256), 0, s,
+                         a, chunks);
+    else
+      hipLaunchKernelGGL(kv_write_vec_kernel<false>, dim3(grid_for(chunks, 256)), dim3(256), 0, s,
+                         a, chunks);
+    return check_hip(hipGetLastError(), "kv_write launch");
+  }
   int threads = a.head_dim >= 128 ? 128 : 64;
   hipLaunchKernelGGL(kv_write_kernel, dim3((unsigned)rows), dim3(threads), 0,
                      s, a);
