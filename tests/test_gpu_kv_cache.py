@@ -123,6 +123,26 @@ def test_kv_write_vector_and_element_paths_agree(gpu, fp8):
     assert torch.equal(_bytes(caches[4]), _bytes(caches[0]))
 
 
+def test_kv_write_unaligned_rows_take_the_element_path(gpu):
+    """Contiguous bf16 rows starting 2 bytes past a 16-byte boundary do not
+    meet the vector kernel's alignment: the write still lands bit-exact."""
+    g = torch.Generator().manual_seed(4)
+    nb, H, bs, d, T = 12, 2, 16, 64, 19
+    flat = torch.randn((2, T * H * d + 1), generator=g).to(torch.bfloat16).to(gpu)
+    k = flat[0, 1:].view(T, H, d)
+    v = flat[1, 1:].view(T, H, d)
+    assert k.data_ptr() % 16 != 0
+    slots = torch.randperm(nb * bs, generator=g)[:T]
+    kc = torch.zeros((nb, H, bs, d), dtype=torch.bfloat16)
+    vc = torch.zeros_like(kc)
+    kcd, vcd = kc.to(gpu), vc.to(gpu)
+    K.kv_write(k, v, slots.to(gpu), kcd, vcd)
+    _index_put_ref(kc, k.cpu(), slots, bs)
+    _index_put_ref(vc, v.cpu(), slots, bs)
+    assert torch.equal(_bytes(kcd), _bytes(kc))
+    assert torch.equal(_bytes(vcd), _bytes(vc))
+
+
 def test_kv_write_packed_k(gpu):
     g = torch.Generator().manual_seed(2)
     nb, H, bs, d, T = 10, 2, 16, 64, 21

@@ -779,10 +779,19 @@ constexpr int kDmaIds = dma_ids(kDmaWaves);
 constexpr int waitcnt_vm(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 static_assert(waitcnt_vm(4) == 0xF74 && waitcnt_vm(0) == 0xF70, "vmcnt encoding");
 
-template <int D, int WAVES, int STAGES>
+// FP8 = true (e4m3fn cache): the ring holds the FP8 tiles as copied (a
+// 64-key tile is 64 x 128 contiguous bytes of its block in both K layouts);
+// every step all threads widen the next tile into one of two bf16 tile
+// buffers in the layout the products read (one 16-byte FP8 chunk of K and
+// of V per thread, x 2^-8 as in the register kernel), so the products and
+// softmax are those of the bf16 kernel.  PK: K in the packed layout (a
+// 16-byte chunk holds 8 channels of a token pair, interleaved).
+template <int D, int WAVES, int STAGES, bool FP8, bool PK>
 __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(PrefillKParams p) {
   static_assert(D == 128, "256-byte rows");
   static_assert((WAVES == 8 || WAVES == 4) && (STAGES == 2 || STAGES == 3), "ring shape");
+  static_assert(!FP8 || (WAVES == 8 && STAGES == 3), "FP8 ring: one chunk per thread");
+  static_assert(FP8 || !PK, "packed K is an FP8 layout");
   constexpr int kDmaWaves = WAVES;
   constexpr int kDmaRows = dma_rows(WAVES);
   constexpr int kDmaIds = dma_ids(WAVES);
@@ -791,6 +800,9 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   constexpr int ROWB = D * 2;          // bytes per K/V row
   constexpr int TILEB = kKT * ROWB;    // bytes per K (or V) tile
   constexpr int NJ = 16 / kDmaWaves;   // DMA instructions per thread per tile (K and V each)
+  constexpr int EB = FP8 ? 1 : 2;      // cache bytes per element
+  constexpr int TILE8 = kKT * D;       // bytes per FP8 K (or V) tile
+  constexpr int NJ8 = 8 / kDmaWaves;   // FP8 DMA instructions per thread per tile
   typedef short s16x4_t __attribute__((ext_vector_type(4)));
   typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
   typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
@@ -798,7 +810,10 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   // byte offset of each block of the workgroup's key range (K and V share
   // the block and token strides on this path)
   __shared__ __attribute__((aligned(16))) int64_t offs_lds[kDmaIds];
-  __shared__ __attribute__((aligned(1024))) uint8_t kv_lds[STAGES][2][TILEB];  // [stage][K, V]
+  // bf16: [stage][K, V] tiles of the ring; FP8: [buffer][K, V] bf16 tiles
+  // the products read, the FP8 ring in kv8_lds
+  __shared__ __attribute__((aligned(1024))) uint8_t kv_lds[FP8 ? 2 : STAGES][2][TILEB];
+  __shared__ __attribute__((aligned(1024))) uint8_t kv8_lds[FP8 ? STAGES : 1][2][FP8 ? TILE8 : 16];
   // LDS addresses are handled as LDS pointers / integers only: a generic
   // pointer to shared memory carried through the loops would need the
   // aperture conversion at every use
@@ -868,7 +883,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
     for (int i = tid; i <= b_hi - b_lo; i += WAVES * 64) {
       int32_t v = p.bt[bt_row + (int64_t)(b_lo + i) * p.bt_j];
       v = v < 0 ? 0 : (v >= p.nb ? p.nb - 1 : v);
-      offs_lds[i] = (int64_t)v * p.kc_blk * 2;
+      offs_lds[i] = (int64_t)v * p.kc_blk * EB;
     }
   }
   // Q (its loads share the round trip of the block ids) scaled and rounded
@@ -1016,7 +1031,113 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   // stay in flight: 2 * NJ instructions per tile), then the barrier makes
   // every thread's copies visible and guarantees that the stage of tile
   // kt - 64, which the step refills, is no longer read.
-  if (any_key) {
+  if constexpr (FP8) {
+    if (any_key) {
+      // ---- FP8 copies: instruction j of wave w covers rows 8q .. 8q+7,
+      // q = 8j + w; lane -> row 8q + lane/8, 16-byte chunk lane % 8, row-major
+      // in the stage (block_size % 8 == 0: the 8 rows share a block)
+      const uint8_t *k_head = p.k_cache + (int64_t)h * p.kc_h;
+      const uint8_t *v_head = p.v_cache + (int64_t)h * p.vc_h;
+      int32_t lane8[NJ8];
+      int jblk8[NJ8];
+#pragma unroll
+      for (int j = 0; j < NJ8; ++j) {
+        const int row = 8 * (kDmaWaves * j + wave) + (lane >> 3);
+        lane8[j] = (row % p.bs) * (int)p.kc_t + ((lane & 7) << 4);
+        jblk8[j] = p.bs <= kKT ? (8 * (kDmaWaves * j + wave)) / p.bs : 0;
+      }
+      typedef __attribute__((address_space(3))) uint8_t lds_u8_t8;
+      const uint32_t lds8 = (uint32_t)(uintptr_t)(lds_u8_t8 *)&kv8_lds[0][0][0];
+      auto issue8 = [&](int kt, int stg) {
+        const int kt_blk = (int)fdiv((uint32_t)kt, p.bs_div);
+        const int ktb = (kt - kt_blk * p.bs) * (int)p.kc_t;
+        const uint32_t k_dst = lds8 + (uint32_t)(stg * 2 * TILE8), v_dst = k_dst + TILE8;
+#pragma unroll
+        for (int j = 0; j < NJ8; ++j) {
+          const int q = kDmaWaves * j + wave;
+          const int bi = min(kt_blk + jblk8[j], p.nblk - 1) - b_lo;
+          const int64_t o = offs_lds[bi];
+          const int64_t off =
+              (int64_t)(((uint64_t)(uint32_t)readfirstlane((int)(o >> 32)) << 32) |
+                        (uint32_t)readfirstlane((int)o)) + ktb;
+          dma16(k_head + off + lane8[j], k_dst + q * 1024);
+          dma16(v_head + off + lane8[j], v_dst + q * 1024);
+        }
+      };
+      // widen FP8 tile of stage stg into bf16 buffer bb: thread t takes row
+      // t / 8, FP8 chunk t % 8 (channels 16c' .. 16c'+15 = bf16 chunks 2c',
+      // 2c'+1), written at the swizzled places the products read
+      typedef __attribute__((address_space(3))) u32x4_t lds_u32x4_t;
+      auto widen = [&](int stg, int bb) {
+        const lds_u8_t8 *s8 = (const lds_u8_t8 *)&kv8_lds[stg][0][0];
+        lds_u8_t *kb = kv_base + bb * 2 * TILEB;
+        lds_u8_t *vb = kb + TILEB;
+        {  // V (and unpacked K): row t / 8, FP8 chunk t % 8 = bf16 chunks 2c', 2c'+1
+          const int row = tid >> 3, c8 = tid & 7;
+#pragma unroll
+          for (int kv = PK ? 1 : 0; kv < 2; ++kv) {
+            const u32x4_t w = *(const lds_u32x4_t *)(s8 + kv * TILE8 + row * D + (c8 << 4));
+            const u32x4_t lo = e4m3fn_x8_to_bf16_scaled(u32x2_t{w[0], w[1]});
+            const u32x4_t hi = e4m3fn_x8_to_bf16_scaled(u32x2_t{w[2], w[3]});
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) {
+              const int c = 2 * c8 + hh;
+              const int sw = kv == 0 ? (c ^ (row & 15)) : (c ^ ((row & 3) << 2));
+              *(lds_u32x4_t *)((kv == 0 ? kb : vb) + row * ROWB + (sw << 4)) = hh == 0 ? lo : hi;
+            }
+          }
+        }
+        if constexpr (PK) {  // packed K: token pair t / 16, channels 8c'..8c'+7, c' = t % 16
+          const int pr = tid >> 4, c = tid & 15;
+          const u32x4_t w = *(const lds_u32x4_t *)(s8 + pr * 2 * D + (c << 4));
+#pragma unroll
+          for (int o = 0; o < 2; ++o) {
+            const int row = 2 * pr + o;
+            *(lds_u32x4_t *)(kb + row * ROWB + ((c ^ (row & 15)) << 4)) = e4m3fn_x8_to_bf16_scaled(
+                packed_pair_pick(w, o == 0 ? kPackedSelEven : kPackedSelOdd));
+          }
+        }
+      };
+      // Ring of STAGES FP8 stages, two bf16 buffers.  At the top of the
+      // step of tile kt this thread waits for its copies of tile kt + 64;
+      // the barrier then makes every copy of it and every widened element
+      // of tile kt visible, and frees the bf16 buffer of tile kt - 64 and
+      // the FP8 stage of tile kt (widened one step earlier).
+      const int n_t = (kt_last - kt0) / kKT + 1;
+#pragma unroll
+      for (int i = 0; i < STAGES; ++i)
+        if (i < n_t) issue8(kt0 + i * kKT, i);
+      {
+        const int later = min(STAGES, n_t) - 1;  // tiles issued after the first
+        if (later >= 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(4 * NJ8));
+        else if (later == 1) __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * NJ8));
+        else __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+      }
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      widen(0, 0);
+      int t = 0;
+      for (int kt = kt0; kt <= kt_last; kt += kKT, ++t) {
+        const bool has_next = kt + kKT <= kt_last;
+        if (has_next) {
+          if (kt + 2 * kKT <= kt_last)
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * NJ8));  // tile kt + 128 stays in flight
+          else
+            __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+        }
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        const int st_c = t % STAGES;  // stage of tile kt (free: widened last step)
+        if (has_next) widen((t + 1) % STAGES, (t + 1) & 1);
+        const lds_u8_t *kb = kv_base + (t & 1) * 2 * TILEB;
+        compute_tile(kt, kb, kb + TILEB, [&]() {
+          if (kt + STAGES * kKT <= kt_last) issue8(kt + STAGES * kKT, st_c);
+        });
+      }
+    }
+  } else if (any_key) {
     const uint32_t lds0 = (uint32_t)(uintptr_t)kv_base;
     auto k_at = [&](int stg) { return lds0 + (uint32_t)(stg * 2 * TILEB); };
     constexpr int kAhead = STAGES - 1;  // tiles in flight beside the one computed
@@ -1046,7 +1167,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   }
 
   finish_rows<D>(p, acc_o, rm.final_max(), l_run, row_ok, seq, h, hq, (int64_t)q_begin + pos_r,
-                 r, half, kr.n_sp, sp, p.v_deq ? p.v_deq[h] : 1.0f);
+                 r, half, kr.n_sp, sp, (p.v_deq ? p.v_deq[h] : 1.0f) * (FP8 ? 256.0f : 1.0f));
 }
 
 // ---------------------------------------------------------------------------
@@ -1149,9 +1270,14 @@ int device_cus() {
 }
 
 bool use_dma_kernel(const mia_prefill_args &a) {
-  return a.head_dim == 128 && a.cache_dtype == MIA_DTYPE_BF16 && a.block_size % 16 == 0 &&
+  const bool dtype_ok = a.cache_dtype == MIA_DTYPE_BF16 || a.cache_dtype == MIA_DTYPE_FP8_E4M3FN;
+  // the copies address K and V with one block offset and one token stride
+  // (packed K: the stride of the even token of a pair)
+  const int64_t k_tok = a.k_packed ? a.k_cache_stride[2] / 2 : a.k_cache_stride[2];
+  return a.head_dim == 128 && dtype_ok && a.block_size % 16 == 0 &&
+         k_tok == a.v_cache_stride[2] &&
          (64 % a.block_size == 0 || a.block_size % 64 == 0) && a.blocks_per_seq <= kDmaIds &&
-         a.k_cache_stride[0] == a.v_cache_stride[0] && a.k_cache_stride[2] == a.v_cache_stride[2];
+         a.k_cache_stride[0] == a.v_cache_stride[0];
 }
 
 }  // namespace
@@ -1265,8 +1391,15 @@ int launch_paged_prefill(const mia_prefill_args &a, const PrefillPlan &pl, hipSt
   const dim3 grid((unsigned)((pl.rows_max + pl.rows_wg - 1) / pl.rows_wg),
                   (unsigned)a.num_kv_heads, (unsigned)(pl.nsplit * a.num_seqs));
   if (pl.dma) {
-    hipLaunchKernelGGL((prefill_dma_kernel<128, kDmaWaves, kDmaStages>), grid,
-                       dim3(kDmaWaves * 64), 0, s, kp);
+    if (fp8 && a.k_packed)
+      hipLaunchKernelGGL((prefill_dma_kernel<128, kDmaWaves, kDmaStages, true, true>), grid,
+                         dim3(kDmaWaves * 64), 0, s, kp);
+    else if (fp8)
+      hipLaunchKernelGGL((prefill_dma_kernel<128, kDmaWaves, kDmaStages, true, false>), grid,
+                         dim3(kDmaWaves * 64), 0, s, kp);
+    else
+      hipLaunchKernelGGL((prefill_dma_kernel<128, kDmaWaves, kDmaStages, false, false>), grid,
+                         dim3(kDmaWaves * 64), 0, s, kp);
   } else if (a.head_dim == 128) {
     if (a.k_packed) hipLaunchKernelGGL((prefill_kernel<128, true, true>), grid, dim3(256), 0, s, kp);
     else if (fp8) hipLaunchKernelGGL((prefill_kernel<128, true, false>), grid, dim3(256), 0, s, kp);
