@@ -231,16 +231,24 @@ def test_split_keys_match_unsplit_and_reference(gpu, case, split):
         assert err <= tol, (i, err)
 
 
-def test_copy_ring_and_register_kernels_agree(gpu):
-    """A bf16 d = 128 cache runs the copy-ring kernel, whose copies share the
-    block offsets of K and V; a V cache with its own block stride (a view of
-    a wider allocation) takes the register-staged kernel.  Both match float64
-    math, and each other to within two bf16 steps."""
+@pytest.mark.parametrize("fp8", [False, True])
+def test_copy_ring_and_register_kernels_agree(gpu, fp8):
+    """A d = 128 cache (bf16, or FP8 widened in the ring) runs the copy-ring
+    kernel, whose copies share the block offsets of K and V; a V cache with
+    its own block stride (a view of a wider allocation) takes the
+    register-staged kernel.  Both match float64 math, and each other to
+    within two bf16 steps."""
     priors = [700, 96]
     cfg = W.PrefillConfig("r", len(priors), 16, 4, 128, 32, 160, max(priors), max(priors),
-                          seed=131)
+                          fp8=fp8, seed=131)
     b = W.make_prefill_batch(cfg, gpu)
-    K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache)
+    kw = {}
+    if fp8:
+        kw = dict(k_dequant=b.k_dequant, v_dequant=b.v_dequant)
+        K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache, quant_mode=2,
+                   k_scale=b.k_quant, v_scale=b.v_quant, scale_per_head=True)
+    else:
+        K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache)
     nb, Hkv, bs, d = b.v_cache.shape
     wide = torch.zeros(nb, Hkv + 1, bs, d, dtype=b.v_cache.dtype, device=gpu)
     wide[:, :Hkv].copy_(b.v_cache)
@@ -249,16 +257,20 @@ def test_copy_ring_and_register_kernels_agree(gpu):
     prior = torch.tensor(priors, dtype=torch.int32, device=gpu)
     scale = d ** -0.5
     ring = K.paged_prefill(b.q, b.cu_seqlens, prior, cfg.new_tokens, b.k_cache, b.v_cache,
-                           b.block_table, scale=scale)
+                           b.block_table, scale=scale, **kw)
     regs = K.paged_prefill(b.q, b.cu_seqlens, prior, cfg.new_tokens, b.k_cache, v_view,
-                           b.block_table, scale=scale)
+                           b.block_table, scale=scale, **kw)
     assert (ring.float() - regs.float()).abs().max().item() <= 1.6e-2
+    kc, vc = b.k_cache.cpu(), b.v_cache.cpu()
+    if fp8:
+        kc = kc.float() * b.k_dequant.cpu().view(1, -1, 1, 1)
+        vc = vc.float() * b.v_dequant.cpu().view(1, -1, 1, 1)
     for i, pr in enumerate(priors):
         s0, s1 = int(b.cu_seqlens[i]), int(b.cu_seqlens[i + 1])
         n = pr + (s1 - s0)
-        ks = _seq_kv(b.k_cache.cpu(), b.block_table[i].cpu(), n, Hkv)
-        vs = _seq_kv(b.v_cache.cpu(), b.block_table[i].cpu(), n, Hkv)
+        ks = _seq_kv(kc, b.block_table[i].cpu(), n, Hkv)
+        vs = _seq_kv(vc, b.block_table[i].cpu(), n, Hkv)
         f = OSg.fp32_prefill(b.q[s0:s1].cpu(), ks, vs, pr, scale, 0, None)
         for out in (ring, regs):
             err = (out[s0:s1].float().cpu().double() - f).abs().max().item()
-            assert err <= TOL_BF16, (i, err)
+            assert err <= (TOL_FP8 if fp8 else TOL_BF16), (i, err)
