@@ -12,7 +12,9 @@ the swizzle of the unpacked cache after the same update.
 import pytest
 import torch
 
+from oracle import decode as OD
 from oracle import packed as OP
+from oracle import segmented as OSg
 from vllm_neuron_amd import _kernels as K
 from vllm_neuron_amd import workloads as W
 from vllm_neuron_amd.functional import segmented_attention
@@ -115,6 +117,36 @@ def test_prefill_packed_read_equals_unpacked(gpu, case):
     out = K.paged_prefill(b.q, b.cu_seqlens, b.prior, b.max_seqlen_q, _pack(b.k_cache),
                           b.v_cache, b.block_table, k_packed=True, **kw)
     assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("bs", [16, 32, 128])
+def test_fp8_copy_ring_block_sizes(gpu, bs):
+    """FP8 d = 128 prefill on the copy-ring kernel at block sizes below,
+    equal to and above its 64-key tile (a tile spanning several blocks, or
+    lying inside one): packed K reads equal unpacked reads bit for bit, and
+    both match float64 math on the dequantised cache."""
+    print(f"fp8 copy ring bs={bs}", flush=True)
+    cfg = W.PrefillConfig("t", 2, 16, 2, 128, bs, 200, 700, 700, fp8=True, seed=600 + bs)
+    b = W.make_prefill_batch(cfg, gpu)
+    K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache, quant_mode=2,
+               k_scale=b.k_quant, v_scale=b.v_quant, scale_per_head=True)
+    kw = dict(scale=128 ** -0.5, k_dequant=b.k_dequant, v_dequant=b.v_dequant)
+    ref = K.paged_prefill(b.q, b.cu_seqlens, b.prior, b.max_seqlen_q, b.k_cache, b.v_cache,
+                          b.block_table, **kw)
+    out = K.paged_prefill(b.q, b.cu_seqlens, b.prior, b.max_seqlen_q, _pack(b.k_cache),
+                          b.v_cache, b.block_table, k_packed=True, **kw)
+    assert torch.equal(out, ref)
+    kc = b.k_cache.cpu().float() * b.k_dequant.cpu().view(1, -1, 1, 1)
+    vc = b.v_cache.cpu().float() * b.v_dequant.cpu().view(1, -1, 1, 1)
+    for i in range(cfg.num_seqs):
+        s0, s1 = int(b.cu_seqlens[i]), int(b.cu_seqlens[i + 1])
+        pr = int(b.prior[i])
+        n = pr + (s1 - s0)
+        ks = torch.stack([OD.gather_contiguous(kc, b.block_table[i].cpu(), n, h) for h in range(2)])
+        vs = torch.stack([OD.gather_contiguous(vc, b.block_table[i].cpu(), n, h) for h in range(2)])
+        f = OSg.fp32_prefill(b.q[s0:s1].cpu(), ks, vs, pr, 128 ** -0.5, 0, None)
+        err = (ref[s0:s1].float().cpu().double() - f).abs().max().item()
+        assert err <= 6e-2, (i, err)
 
 
 def test_segmented_attention_fp8_packed(gpu):
