@@ -8,6 +8,8 @@
 //                    residual adds, before the projection
 // Both replace chains of small tensor ops with one pass over the bytes of a
 // projection row: they are HBM- (or launch-) bound, with no reuse to tile.
+#include <algorithm>
+
 #include "mia_device.h"
 #include "mia_internal.h"
 
@@ -50,8 +52,11 @@ MIA_DEV void rotate_pair(float &xa, float &xb, float ca, float sa, float cb, flo
 // Loads and stores are 8 or 16 bytes wide.  The lanes of a row are an
 // aligned group, so its norm reduction is a butterfly of xor shuffles inside
 // the group.
+constexpr int kMaxHpg = 4;  // head rows per lane group at most (the host splits beyond)
+
 template <int D>
-__global__ __launch_bounds__(256) void qkv_epilogue_kernel(mia_qkv_epilogue_args a, int hpg) {
+__global__ __launch_bounds__(256) void qkv_epilogue_kernel(mia_qkv_epilogue_args a, int hpg,
+                                                            int cs_vec) {
   constexpr int P = D / 2;
   constexpr int NP = 4;
   constexpr int L = P / NP;
@@ -65,37 +70,65 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(mia_qkv_epilogue_args
   // element of pair i: ea(i), eb(i); its pair index is 4j + i in both layouts
   auto ea = [&](int i) { return inter ? 8 * j + 2 * i : 4 * j + i; };
   auto eb = [&](int i) { return inter ? 8 * j + 2 * i + 1 : P + 4 * j + i; };
+  // The raw bf16 pairs of this group's head rows (up to kMaxHpg) are loaded
+  // first, all in flight together, then processed row by row.
+  const int h0 = blockIdx.y * G * hpg + grp;
+  u32x4_t raw[kMaxHpg];  // interleaved: 8 elements; half split: 4 + 4
+#pragma unroll
+  for (int k = 0; k < kMaxHpg; ++k) {
+    raw[k] = u32x4_t{0u, 0u, 0u, 0u};
+    const int hh = h0 + k * G;
+    if (k < hpg && hh < NH) {
+      const uint16_t *xr = (const uint16_t *)a.qkv + t * a.qkv_stride + (int64_t)hh * D;
+      if (inter) {
+        raw[k] = *reinterpret_cast<const u32x4_t *>(xr + 8 * j);
+      } else {
+        const u32x2_t wa = *reinterpret_cast<const u32x2_t *>(xr + 4 * j);
+        const u32x2_t wb = *reinterpret_cast<const u32x2_t *>(xr + P + 4 * j);
+        raw[k] = u32x4_t{wa[0], wa[1], wb[0], wb[1]};
+      }
+    }
+  }
   float rc_a[NP], rs_a[NP], rc_b[NP], rs_b[NP];  // this lane's cos / sin of token t
   if (a.rope_mode != 0) {
     const float *cr = a.cos + t * a.cos_stride[0];
     const float *sr = a.sin + t * a.sin_stride[0];
+    if (cs_vec) {
+      // 16-byte loads of 4 consecutive values (contiguous, aligned tables)
+      const int pj = 4 * j;
+      const float4 ca = *reinterpret_cast<const float4 *>(cr + pj);
+      const float4 sa = *reinterpret_cast<const float4 *>(sr + pj);
+      const float4 cb = *reinterpret_cast<const float4 *>(cr + pj + a.cos_hi_off);
+      const float4 sb = *reinterpret_cast<const float4 *>(sr + pj + a.sin_hi_off);
+      rc_a[0] = ca.x; rc_a[1] = ca.y; rc_a[2] = ca.z; rc_a[3] = ca.w;
+      rs_a[0] = sa.x; rs_a[1] = sa.y; rs_a[2] = sa.z; rs_a[3] = sa.w;
+      rc_b[0] = cb.x; rc_b[1] = cb.y; rc_b[2] = cb.z; rc_b[3] = cb.w;
+      rs_b[0] = sb.x; rs_b[1] = sb.y; rs_b[2] = sb.z; rs_b[3] = sb.w;
+    } else {
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      const int pj = 4 * j + i;
-      rc_a[i] = cr[(int64_t)pj * a.cos_stride[1]];
-      rs_a[i] = sr[(int64_t)pj * a.sin_stride[1]];
-      rc_b[i] = cr[(int64_t)(pj + a.cos_hi_off) * a.cos_stride[1]];
-      rs_b[i] = sr[(int64_t)(pj + a.sin_hi_off) * a.sin_stride[1]];
+      for (int i = 0; i < NP; ++i) {
+        const int pj = 4 * j + i;
+        rc_a[i] = cr[(int64_t)pj * a.cos_stride[1]];
+        rs_a[i] = sr[(int64_t)pj * a.sin_stride[1]];
+        rc_b[i] = cr[(int64_t)(pj + a.cos_hi_off) * a.cos_stride[1]];
+        rs_b[i] = sr[(int64_t)(pj + a.sin_hi_off) * a.sin_stride[1]];
+      }
     }
   }
 
-  auto do_row = [&](int hh) {
+  auto do_row = [&](int hh, const u32x4_t &w) {
     const int kind = hh < Hq ? 0 : (hh < Hq + Hkv ? 1 : 2);  // Q, K, V
     const int h = kind == 0 ? hh : (kind == 1 ? hh - Hq : hh - Hq - Hkv);
 
     float xa[NP], xb[NP];
-    const uint16_t *xr = (const uint16_t *)a.qkv + t * a.qkv_stride + (int64_t)hh * D;
     if (inter) {
-      const u32x4_t w = *reinterpret_cast<const u32x4_t *>(xr + 8 * j);
 #pragma unroll
       for (int i = 0; i < NP; ++i) { xa[i] = bf16lo(w[i]); xb[i] = bf16hi(w[i]); }
     } else {
-      const u32x2_t wa = *reinterpret_cast<const u32x2_t *>(xr + 4 * j);
-      const u32x2_t wb = *reinterpret_cast<const u32x2_t *>(xr + P + 4 * j);
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
-        xa[2 * i] = bf16lo(wa[i]); xa[2 * i + 1] = bf16hi(wa[i]);
-        xb[2 * i] = bf16lo(wb[i]); xb[2 * i + 1] = bf16hi(wb[i]);
+        xa[2 * i] = bf16lo(w[i]); xa[2 * i + 1] = bf16hi(w[i]);
+        xb[2 * i] = bf16lo(w[2 + i]); xb[2 * i + 1] = bf16hi(w[2 + i]);
       }
     }
 
@@ -226,11 +259,11 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(mia_qkv_epilogue_args
           cb[0] | (cb[1] << 8) | (cb[2] << 16) | (cb[3] << 24);
     }
   };
-  const int h0 = blockIdx.y * G * hpg + grp;
-  for (int k = 0; k < hpg; ++k) {
+#pragma unroll
+  for (int k = 0; k < kMaxHpg; ++k) {
     const int hh = h0 + k * G;
-    if (hh >= NH) break;  // uniform in the group of the row
-    do_row(hh);
+    if (k >= hpg || hh >= NH) break;  // uniform in the group of the row
+    do_row(hh, raw[k]);
   }
 
 }
@@ -374,12 +407,17 @@ int launch_qkv_epilogue(const mia_qkv_epilogue_args &a, hipStream_t s) {
   const int nh = a.num_q_heads + 2 * a.num_kv_heads;
   const int groups = 256 / (a.head_dim / 8);
   const int per_wg = a.num_tokens >= 1024 ? nh : groups;
-  const int hpg = (per_wg + groups - 1) / groups;
+  const int hpg = std::min(kMaxHpg, (per_wg + groups - 1) / groups);
   const dim3 grid((unsigned)a.num_tokens, (unsigned)((nh + groups * hpg - 1) / (groups * hpg)));
+  // cos / sin rows read 16 bytes at a time when contiguous and aligned
+  auto al16 = [](const void *q) { return ((uintptr_t)q & 15) == 0; };
+  const int cs_vec = a.rope_mode != 0 && a.cos_stride[1] == 1 && a.sin_stride[1] == 1 &&
+                     al16(a.cos) && al16(a.sin) && a.cos_stride[0] % 4 == 0 &&
+                     a.sin_stride[0] % 4 == 0 && a.cos_hi_off % 4 == 0 && a.sin_hi_off % 4 == 0;
   if (a.head_dim == 128)
-    hipLaunchKernelGGL(qkv_epilogue_kernel<128>, grid, dim3(256), 0, s, a, hpg);
+    hipLaunchKernelGGL(qkv_epilogue_kernel<128>, grid, dim3(256), 0, s, a, hpg, cs_vec);
   else
-    hipLaunchKernelGGL(qkv_epilogue_kernel<64>, grid, dim3(256), 0, s, a, hpg);
+    hipLaunchKernelGGL(qkv_epilogue_kernel<64>, grid, dim3(256), 0, s, a, hpg, cs_vec);
   return check_hip(hipGetLastError(), "qkv epilogue launch");
 }
 
