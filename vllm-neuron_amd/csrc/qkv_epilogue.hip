@@ -259,11 +259,15 @@ __global__ __launch_bounds__(256) void qkv_epilogue_kernel(mia_qkv_epilogue_args
           cb[0] | (cb[1] << 8) | (cb[2] << 16) | (cb[3] << 24);
     }
   };
-#pragma unroll
-  for (int k = 0; k < kMaxHpg; ++k) {
+  // one copy of the row code (the rows shift down the loaded registers): the
+  // kernel stays small enough for the instruction cache
+#pragma nounroll
+  for (int k = 0; k < hpg; ++k) {
     const int hh = h0 + k * G;
-    if (k >= hpg || hh >= NH) break;  // uniform in the group of the row
-    do_row(hh, raw[k]);
+    if (hh >= NH) break;  // uniform in the group of the row
+    do_row(hh, raw[0]);
+#pragma unroll
+    for (int m = 0; m + 1 < kMaxHpg; ++m) raw[m] = raw[m + 1];
   }
 
 }
