@@ -864,37 +864,44 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   // Q pre-multiplied by the softmax scale (log2 units) and rounded to bf16,
   // so that the MFMA yields scaled scores and the softmax needs no multiply
   const float scale2 = p.scale_log2 * (p.k_deq ? p.k_deq[h] : 1.0f);
-  u32x4_t qw[KSTEPS];  // raw bf16 Q, scaled once the block offsets are staged
-  {
-    const uint16_t *qp = p.q + (int64_t)(q_begin + (row_ok ? pos_r : 0)) * p.qs_t +
-                         (int64_t)(row_ok ? hq : 0) * p.qs_h;
-#pragma unroll
-    for (int ks = 0; ks < KSTEPS; ++ks) {
-      qw[ks] = u32x4_t{0u, 0u, 0u, 0u};  // zero query: uniform row, scores 0
-      if (row_ok && !uni) qw[ks] = *reinterpret_cast<const u32x4_t *>(qp + ks * 16 + half * 8);
-    }
-  }
+  // ---- byte offsets of blocks b_lo .. b_hi (ids clamped into the pool).
+  // The first block id of each thread is loaded before Q, so that the wait
+  // for it leaves the Q loads in flight.
   const int64_t bt_row = (int64_t)seq * p.bt_s + (int64_t)h * p.bt_h;
-
-  // ---- byte offsets of blocks b_lo .. b_hi (ids clamped into the pool)
   const int b_lo = (int)fdiv((uint32_t)kt0, p.bs_div);
   const int b_hi = min((int)fdiv((uint32_t)(kt_last + kKT - 1), p.bs_div), p.nblk - 1);
-  if (any_key) {
-    for (int i = tid; i <= b_hi - b_lo; i += WAVES * 64) {
-      int32_t v = p.bt[bt_row + (int64_t)(b_lo + i) * p.bt_j];
-      v = v < 0 ? 0 : (v >= p.nb ? p.nb - 1 : v);
-      offs_lds[i] = (int64_t)v * p.kc_blk * EB;
-    }
-  }
-  // Q (its loads share the round trip of the block ids) scaled and rounded
-  // here, before the copy ring starts: a wait placed by the compiler inside
-  // the loop would also drain the in-flight copies
-  bf16x8_t qf[KSTEPS];
+  const int n_blk = any_key ? b_hi - b_lo + 1 : 0;
+  const int32_t bt0 = tid < n_blk ? p.bt[bt_row + (int64_t)(b_lo + tid) * p.bt_j] : 0;
+  auto blk_off = [&](int32_t v) {
+    v = v < 0 ? 0 : (v >= p.nb ? p.nb - 1 : v);
+    return (int64_t)v * p.kc_blk * EB;
+  };
+  // raw bf16 Q, loaded by every lane (rows past the sequence read token 0,
+  // which exists: the launch returns early without tokens) and scaled once
+  // the first copies are in flight
+  u32x4_t qw[KSTEPS];
+  {
+    const uint16_t *qp = p.q + (int64_t)(row_ok ? q_begin + pos_r : 0) * p.qs_t +
+                         (int64_t)(row_ok ? hq : 0) * p.qs_h;
 #pragma unroll
-  for (int ks = 0; ks < KSTEPS; ++ks) {
-    qf[ks] = scale_q8(qw[ks], scale2);
-    asm volatile("" ::"v"(qf[ks]));
+    for (int ks = 0; ks < KSTEPS; ++ks)
+      qw[ks] = *reinterpret_cast<const u32x4_t *>(qp + ks * 16 + half * 8);
   }
+  if (tid < n_blk) offs_lds[tid] = blk_off(bt0);
+  for (int i = tid + WAVES * 64; i < n_blk; i += WAVES * 64)
+    offs_lds[i] = blk_off(p.bt[bt_row + (int64_t)(b_lo + i) * p.bt_j]);
+  // Q scaled and rounded after the first copies are issued (its wait then
+  // overlaps theirs) and before the loop: a wait placed by the compiler
+  // inside the loop would also drain the in-flight copies.  Rows that are
+  // not computed (or attend uniformly) get a zero query.
+  bf16x8_t qf[KSTEPS];
+  auto scale_q = [&]() {
+#pragma unroll
+    for (int ks = 0; ks < KSTEPS; ++ks) {
+      qf[ks] = scale_q8(row_ok && !uni ? qw[ks] : u32x4_t{0u, 0u, 0u, 0u}, scale2);
+      asm volatile("" ::"v"(qf[ks]));
+    }
+  };
   __syncthreads();
 
   // ---- DMA: instruction j of wave w covers rows 4q .. 4q+3, q = 8j + w;
@@ -1107,6 +1114,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
 #pragma unroll
       for (int i = 0; i < STAGES; ++i)
         if (i < n_t) issue8(kt0 + i * kKT, i);
+      scale_q();
       {
         const int later = min(STAGES, n_t) - 1;  // tiles issued after the first
         if (later >= 2) __builtin_amdgcn_s_waitcnt(waitcnt_vm(4 * NJ8));
@@ -1144,6 +1152,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
 #pragma unroll
     for (int i = 0; i < kAhead; ++i)
       if (kt0 + i * kKT <= kt_last) issue_tile(kt0 + i * kKT, k_at(i), k_at(i) + TILEB);
+    scale_q();
     int st = 0;
     for (int kt = kt0; kt <= kt_last; kt += kKT) {
       if constexpr (STAGES == 3) {
@@ -1334,7 +1343,8 @@ PrefillPlan plan_prefill(const mia_prefill_args &a) {
 }
 
 int launch_paged_prefill(const mia_prefill_args &a, const PrefillPlan &pl, hipStream_t s) {
-  if (a.num_seqs == 0 || a.max_seqlen_q == 0) return MIA_OK;
+  // no token: nothing to compute (the copy-ring kernel reads token 0 for rows past a sequence)
+  if (a.num_seqs == 0 || a.max_seqlen_q == 0 || a.num_tokens == 0) return MIA_OK;
   const bool fp8 = a.cache_dtype == MIA_DTYPE_FP8_E4M3FN;
   PrefillKParams kp;
   kp.q = (const uint16_t *)a.q;
