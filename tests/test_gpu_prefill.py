@@ -159,6 +159,27 @@ def test_prefill_empty_and_fully_masked(gpu):
     assert (out.float().cpu() - ref.float()).abs().max().item() <= 1e-2
 
 
+@pytest.mark.parametrize("split", [1 << 20, 0])
+def test_long_table_small_blocks(gpu, split):
+    """Block size 16 and a 12288-token prior: unsplit, one key chunk spans
+    772 blocks, more block offsets than the workgroup's threads stage in
+    one pass; split in halves (the default), 416 and 356.  Both match
+    float64 math."""
+    cfg = W.PrefillConfig("long", 1, 8, 2, 128, 16, 64, 12288, 12288, seed=93)
+    b = W.make_prefill_batch(cfg, gpu)
+    K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache)
+    assert b.block_table.shape[1] * 16 >= 12288 + 64
+    scale = 128 ** -0.5
+    out = K.paged_prefill(b.q, b.cu_seqlens, b.prior, 64, b.k_cache, b.v_cache, b.block_table,
+                          scale=scale, split_tokens=split)
+    n = 12288 + 64
+    ks = _seq_kv(b.k_cache.cpu(), b.block_table[0].cpu(), n, 2)
+    vs = _seq_kv(b.v_cache.cpu(), b.block_table[0].cpu(), n, 2)
+    f = OSg.fp32_prefill(b.q.cpu(), ks, vs, 12288, scale, 0, None)
+    err = (out.float().cpu().double() - f).abs().max().item()
+    assert err <= TOL_BF16, err
+
+
 SPLIT_CASES = [
     # q_heads, kv_heads, d, bs, new, priors, window, sink, fp8
     (32, 8, 128, 32, 256, [1500, 96, 700], 0, False, False),   # copy-ring kernel
