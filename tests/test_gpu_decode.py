@@ -108,6 +108,18 @@ def test_decode_multi_token(gpu, S, case):
     assert err <= TOL_BF16, err
 
 
+@pytest.mark.parametrize("S,case", [(16, 0), (16, 4), (8, 1), (8, 7)])
+def test_decode_many_active_tokens(gpu, S, case):
+    """More than four active tokens per row (the widest combine variant, up
+    to 16), bf16 and FP8 caches, against float64 math."""
+    cfg = _small_cfg(**CASES[case])
+    b = _make(cfg, gpu, S=S)
+    out = _run_core(b).float().cpu()
+    ref = _fp32(b, cfg.head_dim ** -0.5)
+    err = (out.double() - ref).abs().max().item()
+    assert err <= (TOL_FP8 if cfg.fp8 else TOL_BF16), err
+
+
 @pytest.mark.parametrize("split", [256, 512, 2048])
 def test_split_invariance(gpu, split):
     cfg = _small_cfg(q_heads=16, kv_heads=2, head_dim=128, block_size=32, ctx_lo=500,

@@ -772,7 +772,7 @@ struct CombineParams {
   uint8_t *v_cache_w;
 };
 
-constexpr int kMaxAct = 16;
+constexpr int kMaxAct = 16;  // active tokens per row at most (validated on the host)
 constexpr int kSplitBatch = 8;
 
 MIA_DEV float quant_roundtrip(const CombineParams &c, float x, int h, const float *qscale) {
@@ -786,7 +786,11 @@ MIA_DEV float quant_roundtrip(const CombineParams &c, float x, int h, const floa
 // together), adds the active keys and the sink, normalises, writes bf16.
 // The wave of column 0 also writes the active rows into the cache when
 // write slots are given (after every split kernel has read the cache).
-template <int D>
+// MAXS bounds the active tokens (s_active <= MAXS): the per-token code is
+// unrolled MAXS times, so the single-token decode gets one compact copy
+// (with 16 copies the kernel outgrows the instruction cache, and a wave
+// skipping 15 of them spends microseconds fetching the branch targets).
+template <int D, int MAXS>
 __global__ __launch_bounds__(64) void decode_combine_kernel(CombineParams c) {
   constexpr int DPL = D / 64;  // d values per lane
   const DecodeKParams &p = c.k;
@@ -807,9 +811,9 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(CombineParams c) {
   const uint16_t *qp = p.q + b * p.qs_b + (int64_t)s_q * p.qs_s + hq * p.qs_h;
 #pragma unroll
   for (int j = 0; j < DPL; ++j) q[j] = bf16_bits_to_f32(qp[lane + 64 * j]);
-  uint32_t kraw[kMaxAct][DPL], vraw[kMaxAct][DPL];
+  uint32_t kraw[MAXS][DPL], vraw[MAXS][DPL];
 #pragma unroll
-  for (int k = 0; k < kMaxAct; ++k) {
+  for (int k = 0; k < MAXS; ++k) {
     if (k < S) {
       const int64_t kb = b * c.kn_b + (int64_t)k * c.kn_s + (int64_t)h * c.kn_h;
       const int64_t vb = b * c.vn_b + (int64_t)k * c.vn_s + (int64_t)h * c.vn_h;
@@ -875,9 +879,9 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(CombineParams c) {
 
   // ---- active keys (the last S slots of the gathered context)
   const float ascale = c.act_scale_log2 * kdeq;
-  float sk[kMaxAct];
+  float sk[MAXS];
 #pragma unroll
-  for (int k = 0; k < kMaxAct; ++k) {
+  for (int k = 0; k < MAXS; ++k) {
     sk[k] = -INFINITY;
     if (k < S) {
       bool ok;
@@ -900,14 +904,14 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(CombineParams c) {
   }
   float bm = fmaxf(M, sink2);
 #pragma unroll
-  for (int k = 0; k < kMaxAct; ++k) bm = fmaxf(bm, sk[k]);
+  for (int k = 0; k < MAXS; ++k) bm = fmaxf(bm, sk[k]);
   const float bmu = (bm == -INFINITY) ? 0.f : bm;
   const float f = __builtin_amdgcn_exp2f(M - bmu);
   L = L * f + __builtin_amdgcn_exp2f(sink2 - bmu);
 #pragma unroll
   for (int j = 0; j < DPL; ++j) acc[j] *= f;
 #pragma unroll
-  for (int k = 0; k < kMaxAct; ++k) {
+  for (int k = 0; k < MAXS; ++k) {
     if (k < S) {
       const float pk = __builtin_amdgcn_exp2f(sk[k] - bmu);
       L += pk;
@@ -924,7 +928,7 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(CombineParams c) {
   if (c.wslots && col == 0) {
     const int64_t max_slot = (int64_t)p.nb * p.bs;
 #pragma unroll
-    for (int k = 0; k < kMaxAct; ++k) {
+    for (int k = 0; k < MAXS; ++k) {
       if (k >= S) break;
       int64_t slot;
       const int64_t si = (int64_t)b * S + k;
@@ -1152,10 +1156,16 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
   cp.k_cache_w = (uint8_t *)a.k_cache;
   cp.v_cache_w = (uint8_t *)a.v_cache;
   const dim3 cgrid((unsigned)pl.ncols, (unsigned)a.num_kv_heads, (unsigned)a.batch);
-  if (a.head_dim == 128)
-    hipLaunchKernelGGL(decode_combine_kernel<128>, cgrid, dim3(64), 0, s, cp);
-  else
-    hipLaunchKernelGGL(decode_combine_kernel<64>, cgrid, dim3(64), 0, s, cp);
+  const int maxs = a.s_active <= 1 ? 1 : (a.s_active <= 4 ? 4 : kMaxAct);
+  if (a.head_dim == 128) {
+    if (maxs == 1) hipLaunchKernelGGL((decode_combine_kernel<128, 1>), cgrid, dim3(64), 0, s, cp);
+    else if (maxs == 4) hipLaunchKernelGGL((decode_combine_kernel<128, 4>), cgrid, dim3(64), 0, s, cp);
+    else hipLaunchKernelGGL((decode_combine_kernel<128, kMaxAct>), cgrid, dim3(64), 0, s, cp);
+  } else {
+    if (maxs == 1) hipLaunchKernelGGL((decode_combine_kernel<64, 1>), cgrid, dim3(64), 0, s, cp);
+    else if (maxs == 4) hipLaunchKernelGGL((decode_combine_kernel<64, 4>), cgrid, dim3(64), 0, s, cp);
+    else hipLaunchKernelGGL((decode_combine_kernel<64, kMaxAct>), cgrid, dim3(64), 0, s, cp);
+  }
   return check_hip(hipGetLastError(), "decode combine launch");
 }
 
