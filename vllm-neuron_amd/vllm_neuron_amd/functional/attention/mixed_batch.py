@@ -11,7 +11,10 @@ composition this function implements and is tested against:
     attention_decode.py:653-1182).
 
 Here the prefill sequences run as one varlen launch and the decode rows as
-one split-K launch, on the caller's stream, sharing the same paged cache.
+one split-K launch, on the caller's stream, sharing the same paged cache;
+the decode rows' K/V are written to the cache by the decode's merge kernel
+(after every decode workgroup has read the cache), not by a separate
+scatter launch.
 The two launches run back to back: the decode is HBM-bound and needs every
 CU to approach the memory roofline (at the Llama-3-8B mixed shape its 60
 rows take 525 / 299 / 203 us on 64 / 128 / 256 CUs), and the two kernels
@@ -94,9 +97,6 @@ def mixed_batch_attention(
             block_len=block_len, S_ctx=nblk * block_len, pos_ids=decode_pos_ids,
             swa_start_pos_ids=decode_start_pos, sink=sink, softmax_scale=scale,
             k_scale=k_scale, v_scale=v_scale, k_dequant_scale=k_dequant_scale,
-            v_dequant_scale=v_dequant_scale, workspace=decode_workspace)
-        if decode_slots is not None:
-            Bd, S = q_decode.shape[:2]
-            K.kv_write(k_decode.reshape(Bd * S, kv_heads, d), v_decode.reshape(Bd * S, kv_heads, d),
-                       decode_slots, K_cache, V_cache, **qkw)
+            v_dequant_scale=v_dequant_scale, workspace=decode_workspace,
+            write_slots=None if decode_slots is None else decode_slots.reshape(-1))
     return out_d, out_p
