@@ -312,3 +312,88 @@ def test_rows_without_prior_keys(gpu, fp8):
     ref = _fp32(b, cfg.head_dim ** -0.5)
     err = (out.double() - ref).abs().max().item()
     assert err <= (TOL_FP8 if fp8 else TOL_BF16), err
+
+
+# ---- one-pass kernel: tables of at most 8 tiles (256 tokens) take one wave
+# per (row, kv head) segment that also merges the active keys and the sink;
+# split_tokens > 0 forces the split-K kernel and its combine on the same input
+
+@pytest.mark.parametrize("S", [1, 3])
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_one_pass_matches_split_and_reference(gpu, case, S):
+    """Short tables (<= 256 tokens): the one-pass kernel against float64
+    math and against the split-K path on the same inputs, every decode
+    configuration (GQA 1-8, d 64 / 128, block sizes 16-64, sinks, sliding
+    window, FP8), one and three active tokens."""
+    cfg = _small_cfg(**dict(CASES[case], ctx_lo=1, ctx_hi=200, max_model_len=0))
+    b = _make(cfg, gpu, S=S)
+    if b.start is not None:
+        b.start = torch.clamp(b.pos - cfg.window + 1, min=0)
+    S_ctx = b.block_table.shape[-1] * cfg.block_size
+    assert S_ctx <= 256
+    one = _run_core(b).float().cpu()
+    split = _run_core(b, split_tokens=32).float().cpu()
+    ref = _fp32(b, cfg.head_dim ** -0.5)
+    tol = TOL_FP8 if cfg.fp8 else TOL_BF16
+    assert (one.double() - ref).abs().max().item() <= tol
+    assert (split.double() - ref).abs().max().item() <= tol
+    # the two paths differ only in the order of the online merges (and so
+    # in the final bf16 rounding): two bf16 steps at |o| ~ 2
+    assert (one - split).abs().max().item() <= (3e-2 if cfg.fp8 else 1.6e-2)
+
+
+@pytest.mark.parametrize("case", [0, 2, 7, 8])
+def test_one_pass_cache_write_matches_scatter(gpu, case):
+    """One-pass decode with write_slots: the attention output equals the call
+    without it, and the cache holds the bytes of the standalone scatter
+    (sentinel and out-of-pool slots skipped)."""
+    from vllm_neuron_amd import _kernels as K
+    cfg = _small_cfg(**dict(CASES[case], ctx_lo=1, ctx_hi=200, max_model_len=0))
+    S = 2
+    b = _make(cfg, gpu, S=S)
+    B, Hkv = cfg.batch, cfg.kv_heads
+    nb, bs = b.k_cache.shape[0], cfg.block_size
+    g = torch.Generator().manual_seed(12)
+    slots = torch.randperm(nb * bs, generator=g)[:B * S].to(torch.int64)
+    slots[0] = -1
+    slots[-1] = nb * bs + 5
+    slots = slots.to(gpu)
+    kc, vc = b.k_cache.clone(), b.v_cache.clone()
+    base = _run_core(b)
+    b.k_cache.copy_(kc)
+    b.v_cache.copy_(vc)
+    fused = _run_core(b, write_slots=slots)
+    assert torch.equal(base, fused)
+    kw = {}
+    if cfg.fp8:
+        from vllm_neuron_amd.functional.attention.attention_decode import (
+            _quant_mode_for, _scale_per_head)
+        kw = dict(quant_mode=_quant_mode_for(b.k_new.dtype, b.k_quant), k_scale=b.k_quant,
+                  v_scale=b.v_quant, scale_per_head=_scale_per_head(b.k_quant, Hkv))
+    K.kv_write(b.k_new.reshape(B * S, Hkv, -1), b.v_new.reshape(B * S, Hkv, -1), slots, kc, vc,
+               **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(b.k_cache.view(torch.uint8), kc.view(torch.uint8))
+    assert torch.equal(b.v_cache.view(torch.uint8), vc.view(torch.uint8))
+
+
+def test_one_pass_full_mask_mode(gpu):
+    """A pre-generated mask read from HBM (mask mode) on a short table takes
+    the one-pass kernel and gives the positions path's result."""
+    cfg = _small_cfg(batch=4, q_heads=32, kv_heads=4, head_dim=64, block_size=32,
+                     ctx_lo=20, ctx_hi=250)
+    b = _make(cfg, gpu)
+    B, Hq = cfg.batch, cfg.q_heads
+    S_ctx = b.block_table.shape[1] * cfg.block_size
+    assert S_ctx <= 256
+    base = _run_core(b)
+    mask = gen_attention_decode_mask(b.pos.reshape(1, -1), B, Hq, 1, S_ctx,
+                                     block_len=cfg.block_size)
+    mask.mul_(1.0)  # in-place edit: the descriptor no longer applies
+    out = paged_decode_core(b.q, b.k_new, b.v_new, b.k_cache, b.v_cache, b.block_table,
+                            block_len=cfg.block_size, S_ctx=S_ctx, attention_mask=mask,
+                            softmax_scale=cfg.head_dim ** -0.5)
+    # mask mode spans the whole table, the positions path ends at the
+    # row's position, so the tiles are dealt to the waves differently and
+    # the merge order differs: one bf16 step at |o| < 2
+    assert (out.float() - base.float()).abs().max().item() <= 8e-3

@@ -41,6 +41,7 @@ struct DecodePlan {
   int ncols;         // columns (query token x head of a GQA group) per launch
   int col_groups;    // launches over column groups
   int grid;          // workgroups of the persistent split-K kernel
+  int one_pass;      // short tables: one wave per segment, no combine launch
   size_t ws_bytes;   // workspace bytes
 };
 DecodePlan plan_decode(const mia_decode_args &a);

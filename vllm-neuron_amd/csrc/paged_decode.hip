@@ -223,6 +223,44 @@ struct KLoad<true> {
   }
 };
 
+// Parameters of the combine kernel (and of the one-pass kernel, which also
+// does the combine's work): the split geometry plus the active rows, the
+// output and the optional cache update.
+struct CombineParams {
+  DecodeKParams k;  // shared geometry (col0 unused)
+  const uint16_t *k_new;
+  const uint16_t *v_new;
+  int64_t kn_b, kn_s, kn_h;
+  int64_t vn_b, vn_s, vn_h;
+  const float *active_mask;  // [S, B, Hq, S] or null
+  const float *sink;         // [Hq] or null
+  const float *v_deq;
+  float act_scale_log2;      // softmax_scale * log2(e)
+  int fp8;                   // cache partials hold v * 2^-8
+  int quant_mode;            // round trip of the active rows (fp8 cache)
+  const float *k_quant;
+  const float *v_quant;
+  int quant_per_head;
+  uint16_t *out;
+  int64_t os_b, os_s, os_h;
+  // fused cache update of the active rows (stage 8), optional
+  const void *wslots;
+  int wslot_dtype;
+  int cache_dtype;
+  int k_packed;              // K cache in the packed FP8 layout
+  uint8_t *k_cache_w;
+  uint8_t *v_cache_w;
+};
+
+MIA_DEV float quant_roundtrip(const CombineParams &c, float x, int h, const float *qscale) {
+  if (c.quant_mode == MIA_QUANT_NONE) return x;
+  const float s = qscale[c.quant_per_head ? h : 0];
+  return e4m3fn_bits_to_f32(quantize_e4m3fn(x, s, c.quant_mode));
+}
+
+MIA_DEV const DecodeKParams &kparams(const DecodeKParams &p) { return p; }
+MIA_DEV const DecodeKParams &kparams(const CombineParams &c) { return c.k; }
+
 // ---------------------------------------------------------------------------
 // split kernel
 // ---------------------------------------------------------------------------
@@ -302,9 +340,16 @@ MIA_DEV int wave_scan_incl(int x, int lane) {
   return x;
 }
 
-// PK: the K cache is in the packed FP8 layout (FP8 only).
-template <int D, int NCP, bool FP8, bool PK>
-__global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(DecodeKParams p) {
+// PK: the K cache is in the packed FP8 layout (FP8 only).  ONE: one-pass
+// mode (decode_onepass_kernel, P = CombineParams) for tables of at most
+// kOnePassTiles tiles: workgroup g takes segment (b, h) = (g / Hkv, g % Hkv),
+// its four waves stream contiguous runs of the segment's tiles, and the
+// first wave merges their (m, l, o) through LDS, adds the active keys and
+// the sink, normalises and stores the bf16 output: no shares, no global
+// partials, no combine launch.
+template <int D, int NCP, bool FP8, bool PK, bool ONE, typename P>
+MIA_DEV void split_body(const P &c) {
+  const DecodeKParams &p = kparams(c);
   static_assert(FP8 || !PK, "packed K is an FP8 layout");
   constexpr int EB = FP8 ? 1 : 2;      // cache element bytes
   constexpr int KSTEPS = D / 32;
@@ -327,51 +372,58 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
   __shared__ int s_lo[kMaxRows];
   __shared__ int s_hi[kMaxRows];
   __shared__ float s_minpos[kMaxRows];
+  __shared__ float s_one_m[kWaves][16], s_one_l[kWaves][16];  // one-pass merge
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
 
-  // ---- setup (every workgroup): prior range of each row and the prefix
-  // sum R of its tiles over the kv heads
-  for (int r = threadIdx.x; r < p.B; r += kWaves * 64) {
-    const RowInfo ri = row_info(p.pos, p.start, p.mask_mode, p.S, p.s_ctx, r);
-    s_lo[r] = ri.lo;
-    s_hi[r] = ri.hi;
-    s_minpos[r] = ri.minpos;
-  }
-  __syncthreads();
-  if (wave == 0) {
-    int carry = 0;
-    if (lane == 0) s_R[0] = 0;
-    for (int r0 = 0; r0 < p.B; r0 += 64) {
-      const int r = r0 + lane;
-      int n = 0;
-      if (r < p.B && s_lo[r] < s_hi[r])
-        n = ((s_hi[r] + kTile - 1) / kTile - s_lo[r] / kTile) * p.Hkv;
-      const int incl = wave_scan_incl(n, lane) + carry;
-      if (r < p.B) s_R[r + 1] = incl;
-      carry = __shfl(incl, 63, 64);
+  int n_tiles = 0, n_waves = 0, w_id = 0, x_begin = 0, x_end = 0;
+  if constexpr (!ONE) {
+    // ---- setup (every workgroup): prior range of each row and the prefix
+    // sum R of its tiles over the kv heads
+    for (int r = threadIdx.x; r < p.B; r += kWaves * 64) {
+      const RowInfo ri = row_info(p.pos, p.start, p.mask_mode, p.S, p.s_ctx, r);
+      s_lo[r] = ri.lo;
+      s_hi[r] = ri.hi;
+      s_minpos[r] = ri.minpos;
     }
+    __syncthreads();
+    if (wave == 0) {
+      int carry = 0;
+      if (lane == 0) s_R[0] = 0;
+      for (int r0 = 0; r0 < p.B; r0 += 64) {
+        const int r = r0 + lane;
+        int n = 0;
+        if (r < p.B && s_lo[r] < s_hi[r])
+          n = ((s_hi[r] + kTile - 1) / kTile - s_lo[r] / kTile) * p.Hkv;
+        const int incl = wave_scan_incl(n, lane) + carry;
+        if (r < p.B) s_R[r + 1] = incl;
+        carry = __shfl(incl, 63, 64);
+      }
+    }
+    __syncthreads();
+    n_tiles = s_R[p.B];
+    // streaming waves: all of the grid, or fewer so that every share holds at
+    // least min_tiles tiles after rounding (the lightest share is
+    // cls_w[2] / cls_w[0] of the heaviest, and shares are rounded down by
+    // less than one tile)
+    n_waves =
+        max(1, min((int)gridDim.x * kWaves,
+                   (int)((int64_t)n_tiles * p.cls_w[2] /
+                         ((int64_t)p.cls_w[0] * (p.min_tiles + 1)))));
+    if (blockIdx.x == 0) {  // the combine kernel re-derives the slots from these
+      for (int r = threadIdx.x; r <= p.B; r += kWaves * 64) p.ws_hdr[r] = s_R[r];
+      if (threadIdx.x == 0) p.ws_hdr[p.B + 1] = n_waves;
+    }
+    w_id = readfirstlane(blockIdx.x * kWaves + wave);
+    if (n_tiles == 0 || w_id >= n_waves) return;  // no barrier below this point
+    x_begin = (int)share_start(p, w_id, n_tiles, n_waves);
+    x_end = (int)share_start(p, w_id + 1, n_tiles, n_waves);
+    if (x_begin >= x_end) return;
+  } else {
+    w_id = blockIdx.x;  // one (row, kv head) segment per workgroup
+    if (w_id >= p.B * p.Hkv) return;  // uniform: no barrier is skipped
   }
-  __syncthreads();
-  const int n_tiles = s_R[p.B];
-  // streaming waves: all of the grid, or fewer so that every share holds at
-  // least min_tiles tiles after rounding (the lightest share is
-  // cls_w[2] / cls_w[0] of the heaviest, and shares are rounded down by
-  // less than one tile)
-  const int n_waves =
-      max(1, min((int)gridDim.x * kWaves,
-                 (int)((int64_t)n_tiles * p.cls_w[2] /
-                       ((int64_t)p.cls_w[0] * (p.min_tiles + 1)))));
-  if (blockIdx.x == 0) {  // the combine kernel re-derives the slots from these
-    for (int r = threadIdx.x; r <= p.B; r += kWaves * 64) p.ws_hdr[r] = s_R[r];
-    if (threadIdx.x == 0) p.ws_hdr[p.B + 1] = n_waves;
-  }
-  const int w_id = readfirstlane(blockIdx.x * kWaves + wave);
-  if (n_tiles == 0 || w_id >= n_waves) return;  // no barrier below this point
-  const int x_begin = (int)share_start(p, w_id, n_tiles, n_waves);
-  const int x_end = (int)share_start(p, w_id + 1, n_tiles, n_waves);
-  if (x_begin >= x_end) return;
 
   // ---- lane roles
   const int qcol = lane & 15;
@@ -576,7 +628,26 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
     if (lane < nvalid)
       *reinterpret_cast<float2 *>(p.ws_ml + (ws_row + p.col0 + lane) * 2) = make_float2(m, l);
   };
-  Item cur = decode_piece(x_begin, Item{});
+  Item cur;
+  if constexpr (ONE) {
+    const int b = w_id / p.Hkv;
+    const RowInfo ri = row_info(p.pos, p.start, p.mask_mode, p.S, p.s_ctx, b);
+    cur.valid = 1;
+    cur.b = b;
+    cur.h = w_id - b * p.Hkv;
+    cur.j = 0;
+    // the segment's tiles dealt to the workgroup's waves in contiguous runs
+    const int lo = readfirstlane(ri.lo), hi = readfirstlane(ri.hi);
+    const int tf = lo / kTile, nt = hi > lo ? (hi + kTile - 1) / kTile - tf : 0;
+    const int r0 = tf + (nt * wave + kWaves - 1) / kWaves;
+    const int r1 = tf + (nt * (wave + 1) + kWaves - 1) / kWaves;
+    cur.t_lo = max(lo, r0 * kTile);
+    cur.t_hi = max(cur.t_lo, min(hi, r1 * kTile));
+    cur.next_x = 0;
+    cur.minpos = __builtin_bit_cast(float, readfirstlane(__builtin_bit_cast(int, ri.minpos)));
+  } else {
+    cur = decode_piece(x_begin, Item{});
+  }
   bf16x8_t q_cur[KSTEPS];
   load_q(cur, q_cur);
   float st_cur = load_start(cur);
@@ -590,14 +661,20 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
   float st_hold = 0.f, kdq_hold = 1.f;
   kraw_t kr[NSUB][KSTEPS];
   raw_t vr[VPL];
-  {
+  if (!ONE || cur.t_lo < cur.t_hi) {  // a one-pass row may have no prior key
     const TileRef r0 = tile_ref(cur, first_tile(cur));
     issue_k(kr, cur, r0);
     issue_v(vr, cur, r0, first_tile(cur));
   }
 
   while (true) {
-    const Item nxt = decode_piece(cur.next_x, cur);
+    Item nxt;
+    if constexpr (ONE) {
+      nxt = cur;
+      nxt.valid = 0;
+    } else {
+      nxt = decode_piece(cur.next_x, cur);
+    }
     bf16x8_t q_land[KSTEPS];
     load_q(nxt, q_land);
     const float st_land = load_start(nxt);
@@ -726,6 +803,114 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
     // ---- piece epilogue: reduce within the wave, then write the partial
     l_run = wave_sum_xor(l_run, 16);
     l_run = wave_sum_xor(l_run, 32);
+    if constexpr (ONE) {
+      // the segment is whole: merge the active keys and the sink online into
+      // (m_run, l_run, oacc) of the lane's column, normalise, store.  Lane
+      // (qcol, kg) holds q of d = 32 ks + 8 kg + e and O^T of d = 16 blk +
+      // 4 kg + i; the dot products are reduced over the 4 lane groups.
+      // this wave's run: (o, m, l) into its V buffer (free after the last
+      // tile) and s_one_*; the first wave merges the four runs
+      typedef __attribute__((address_space(3))) f32x4_t lds_f32x4_t;
+#pragma unroll
+      for (int blk = 0; blk < DB16; ++blk)
+        *(lds_f32x4_t *)(vw + (qcol * D + 16 * blk + 4 * kg) * 4) = oacc[blk];
+      if (kg == 0) {
+        s_one_m[wave][qcol] = m_run;
+        s_one_l[wave][qcol] = l_run;
+      }
+      __syncthreads();
+      if (wave != 0) return;
+      float m = -INFINITY, l = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) m = fmaxf(m, s_one_m[w][qcol]);
+      {
+        const float mu = (m == -INFINITY) ? 0.f : m;
+#pragma unroll
+        for (int blk = 0; blk < DB16; ++blk) oacc[blk] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) {
+          const float f = __builtin_amdgcn_exp2f(s_one_m[w][qcol] - mu);
+          l += s_one_l[w][qcol] * f;
+          const lds_u8_t *vwo = (lds_u8_t *)&v_lds[w][0];
+#pragma unroll
+          for (int blk = 0; blk < DB16; ++blk) {
+            const f32x4_t o = *(const lds_f32x4_t *)(vwo + (qcol * D + 16 * blk + 4 * kg) * 4);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) oacc[blk][i] += o[i] * f;
+          }
+        }
+      }
+      const int hq = cur.h * p.G + g_q;
+      const float vsc = FP8 ? 256.0f : 1.0f;  // cache V was widened x 2^-8
+#pragma unroll
+      for (int blk = 0; blk < DB16; ++blk)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) oacc[blk][i] *= vsc;
+      auto absorb = [&](float sk, const float (&vv)[DB16][4], bool has_v) {
+        const float m_new = fmaxf(m, sk);
+        const float mu = (m_new == -INFINITY) ? 0.f : m_new;
+        const float a = __builtin_amdgcn_exp2f(m - mu);
+        const float pk = __builtin_amdgcn_exp2f(sk - mu);
+        l = l * a + pk;
+#pragma unroll
+        for (int blk = 0; blk < DB16; ++blk)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            oacc[blk][i] = oacc[blk][i] * a + (has_v ? pk * vv[blk][i] : 0.f);
+        m = m_new;
+      };
+      const float ascale = c.act_scale_log2 * kdq_cur;
+#pragma nounroll
+      for (int k = 0; k < p.S; ++k) {
+        const int64_t kb = cur.b * c.kn_b + (int64_t)k * c.kn_s + (int64_t)cur.h * c.kn_h;
+        const int64_t vb = cur.b * c.vn_b + (int64_t)k * c.vn_s + (int64_t)cur.h * c.vn_h;
+        float dot = 0.f;
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks) {
+          const u32x4_t qw = __builtin_bit_cast(u32x4_t, q_cur[ks]);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float qv = __uint_as_float((e & 1) ? (qw[e >> 1] & 0xffff0000u) : (qw[e >> 1] << 16));
+            const float kv = quant_roundtrip(
+                c, bf16_bits_to_f32(c.k_new[kb + ks * 32 + kg * 8 + e]), cur.h, c.k_quant);
+            dot = fmaf(qv, kv, dot);
+          }
+        }
+        dot = wave_sum_xor(dot, 16);
+        dot = wave_sum_xor(dot, 32);
+        bool ok;
+        if (p.mask_mode == 1) {
+          const int64_t lin = seq_to_linear((int64_t)p.s_ctx - p.S + k, p.mask_bl);
+          ok = p.full_mask[((lin * p.B + cur.b) * p.Hq + hq) * p.S + s_q] != 0.f;
+        } else if (c.active_mask) {
+          ok = c.active_mask[(((int64_t)k * p.B + cur.b) * p.Hq + hq) * p.S + s_q] != 0.f;
+        } else {
+          ok = k <= s_q;
+        }
+        float vv[DB16][4];
+#pragma unroll
+        for (int blk = 0; blk < DB16; ++blk)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            vv[blk][i] = quant_roundtrip(c, bf16_bits_to_f32(c.v_new[vb + 16 * blk + 4 * kg + i]),
+                                         cur.h, c.v_quant);
+        absorb(ok ? dot * ascale : -INFINITY, vv, true);
+      }
+      if (c.sink) {  // the sink logit joins the denominator only
+        const float vz[DB16][4] = {};
+        absorb(c.sink[hq] * kLog2e, vz, false);
+      }
+      if (col_ok) {
+        const float vdeq = c.v_deq ? c.v_deq[cur.h] : 1.0f;
+        uint16_t *op = c.out + cur.b * c.os_b + (int64_t)s_q * c.os_s + hq * c.os_h;
+#pragma unroll
+        for (int blk = 0; blk < DB16; ++blk)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            op[16 * blk + 4 * kg + i] = (uint16_t)f32_to_bf16_bits(oacc[blk][i] / l * vdeq);
+      }
+      break;
+    }
     const int64_t ws_row = (((int64_t)cur.b * p.Hkv + cur.h) * p.num_splits + cur.j) * p.nc_tot;
     write_partial(oacc, m_run, l_run, ws_row, cur.j);
     // the segment's piece count, for the combine, from the piece that ends
@@ -743,43 +928,23 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
   }
 }
 
+template <int D, int NCP, bool FP8, bool PK>
+__global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(DecodeKParams p) {
+  split_body<D, NCP, FP8, PK, false>(p);
+}
+
+template <int D, int NCP, bool FP8, bool PK>
+__global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_onepass_kernel(CombineParams c) {
+  split_body<D, NCP, FP8, PK, true>(c);
+}
+
 // ---------------------------------------------------------------------------
 // combine kernel
 // ---------------------------------------------------------------------------
-struct CombineParams {
-  DecodeKParams k;  // shared geometry (col0 unused)
-  const uint16_t *k_new;
-  const uint16_t *v_new;
-  int64_t kn_b, kn_s, kn_h;
-  int64_t vn_b, vn_s, vn_h;
-  const float *active_mask;  // [S, B, Hq, S] or null
-  const float *sink;         // [Hq] or null
-  const float *v_deq;
-  float act_scale_log2;      // softmax_scale * log2(e)
-  int fp8;                   // cache partials hold v * 2^-8
-  int quant_mode;            // round trip of the active rows (fp8 cache)
-  const float *k_quant;
-  const float *v_quant;
-  int quant_per_head;
-  uint16_t *out;
-  int64_t os_b, os_s, os_h;
-  // fused cache update of the active rows (stage 8), optional
-  const void *wslots;
-  int wslot_dtype;
-  int cache_dtype;
-  int k_packed;              // K cache in the packed FP8 layout
-  uint8_t *k_cache_w;
-  uint8_t *v_cache_w;
-};
 
 constexpr int kMaxAct = 16;  // active tokens per row at most (validated on the host)
 constexpr int kSplitBatch = 8;
 
-MIA_DEV float quant_roundtrip(const CombineParams &c, float x, int h, const float *qscale) {
-  if (c.quant_mode == MIA_QUANT_NONE) return x;
-  const float s = qscale[c.quant_per_head ? h : 0];
-  return e4m3fn_bits_to_f32(quantize_e4m3fn(x, s, c.quant_mode));
-}
 
 // One wave per (column, kv head, batch row): merges the split partials of
 // the row (online, kSplitBatch at a time, all loads of a batch in flight
@@ -978,6 +1143,17 @@ void launch_split_ncp(int ncp, const DecodeKParams &kp, dim3 grid,
   else launch_split<D, 16, FP8, PK>(kp, grid, s);
 }
 
+// one-pass kernel: one four-wave workgroup per (row, kv head) segment
+template <int D, bool FP8, bool PK = false>
+void launch_onepass_ncp(int ncp, const CombineParams &cp, dim3 grid, hipStream_t s) {
+  if (ncp <= 4)
+    hipLaunchKernelGGL((decode_onepass_kernel<D, 4, FP8, PK>), grid, dim3(kWaves * 64), 0, s, cp);
+  else if (ncp <= 8)
+    hipLaunchKernelGGL((decode_onepass_kernel<D, 8, FP8, PK>), grid, dim3(kWaves * 64), 0, s, cp);
+  else
+    hipLaunchKernelGGL((decode_onepass_kernel<D, 16, FP8, PK>), grid, dim3(kWaves * 64), 0, s, cp);
+}
+
 }  // namespace
 
 int decode_noalloc_scratch(void **ptr) {
@@ -1000,6 +1176,9 @@ int decode_noalloc_scratch(void **ptr) {
   *ptr = addr[dev];
   return MIA_OK;
 }
+
+// tables of at most this many 32-token tiles take the one-pass kernel
+constexpr int kOnePassTiles = 8;
 
 DecodePlan plan_decode(const mia_decode_args &a) {
   DecodePlan pl;
@@ -1030,6 +1209,16 @@ DecodePlan plan_decode(const mia_decode_args &a) {
   const int64_t wg = (std::max<int64_t>(1, n_max / mt) + kWaves - 1) / kWaves;
   const int64_t cap = wgs_cu * (int64_t)device_cu_count();
   pl.grid = (int)std::max<int64_t>(1, std::min(wg, cap));
+  // Short tables (sliding-window layers, short contexts): one wave streams
+  // a whole (row, kv head) segment and writes the output itself, saving the
+  // shares, the partials and the combine launch.  A given write_slots is
+  // then served by the cache-write kernel after the attention, which needs
+  // the active rows of the batch as one token sequence.
+  const bool flat_new =
+      a.batch <= 1 || (a.k_new_stride[0] == (int64_t)a.s_active * a.k_new_stride[1] &&
+                       a.v_new_stride[0] == (int64_t)a.s_active * a.v_new_stride[1]);
+  pl.one_pass = a.split_tokens == 0 && t_max <= kOnePassTiles &&
+                (a.write_slots == nullptr || flat_new);
   const size_t rows = (size_t)a.batch * a.num_kv_heads * pl.num_splits * pl.ncols;
   size_t o_bytes = rows * (size_t)a.head_dim * sizeof(float);
   o_bytes = (o_bytes + 255) & ~(size_t)255;
@@ -1097,34 +1286,6 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
   kp.ws_hdr = (int *)((char *)a.workspace + o_bytes + ml_bytes);
   kp.ws_cnt = kp.ws_hdr + (a.batch + 2);
 
-  const dim3 grid((unsigned)pl.grid);
-  if (a.split_event_begin) {
-    int rc = check_hip(hipEventRecord((hipEvent_t)a.split_event_begin, s),
-                       "decode: timing event");
-    if (rc) return rc;
-  }
-  if (pl.num_splits > 0 && kp.s_ctx - kp.S > 0) {
-    for (int cg = 0; cg < pl.col_groups; ++cg) {
-      kp.col0 = cg * 16;
-      const int ncp = std::min(16, pl.ncols - kp.col0);
-      if (a.head_dim == 128) {
-        if (a.k_packed) launch_split_ncp<128, true, true>(ncp, kp, grid, s);
-        else if (fp8) launch_split_ncp<128, true>(ncp, kp, grid, s);
-        else launch_split_ncp<128, false>(ncp, kp, grid, s);
-      } else {
-        if (a.k_packed) launch_split_ncp<64, true, true>(ncp, kp, grid, s);
-        else if (fp8) launch_split_ncp<64, true>(ncp, kp, grid, s);
-        else launch_split_ncp<64, false>(ncp, kp, grid, s);
-      }
-      int rc = check_hip(hipGetLastError(), "decode split launch");
-      if (rc) return rc;
-    }
-  }
-  if (a.split_event_end) {
-    int rc = check_hip(hipEventRecord((hipEvent_t)a.split_event_end, s),
-                       "decode: timing event");
-    if (rc) return rc;
-  }
   kp.col0 = 0;
   CombineParams cp;
   cp.k = kp;
@@ -1156,6 +1317,90 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
   cp.k_cache_w = (uint8_t *)a.k_cache;
   cp.v_cache_w = (uint8_t *)a.v_cache;
   const dim3 cgrid((unsigned)pl.ncols, (unsigned)a.num_kv_heads, (unsigned)a.batch);
+  if (pl.one_pass) {
+    if (a.split_event_begin) {
+      int rc = check_hip(hipEventRecord((hipEvent_t)a.split_event_begin, s),
+                         "decode: timing event");
+      if (rc) return rc;
+    }
+    const dim3 ogrid((unsigned)(a.batch * a.num_kv_heads));
+    for (int cg = 0; cg < pl.col_groups; ++cg) {
+      cp.k.col0 = cg * 16;
+      const int ncp = std::min(16, pl.ncols - cp.k.col0);
+      if (a.head_dim == 128) {
+        if (a.k_packed) launch_onepass_ncp<128, true, true>(ncp, cp, ogrid, s);
+        else if (fp8) launch_onepass_ncp<128, true>(ncp, cp, ogrid, s);
+        else launch_onepass_ncp<128, false>(ncp, cp, ogrid, s);
+      } else {
+        if (a.k_packed) launch_onepass_ncp<64, true, true>(ncp, cp, ogrid, s);
+        else if (fp8) launch_onepass_ncp<64, true>(ncp, cp, ogrid, s);
+        else launch_onepass_ncp<64, false>(ncp, cp, ogrid, s);
+      }
+      int rc = check_hip(hipGetLastError(), "decode one-pass launch");
+      if (rc) return rc;
+    }
+    if (a.split_event_end) {
+      int rc = check_hip(hipEventRecord((hipEvent_t)a.split_event_end, s),
+                         "decode: timing event");
+      if (rc) return rc;
+    }
+    if (!a.write_slots) return MIA_OK;
+    // the active rows of the batch as one token sequence (t = b * S + s)
+    mia_kv_write_args w{};
+    w.k_src = a.k_new;
+    w.v_src = a.v_new;
+    w.src_dtype = MIA_DTYPE_BF16;
+    for (int i = 0; i < 3; ++i) {
+      w.k_src_stride[i] = a.k_new_stride[i + 1];
+      w.v_src_stride[i] = a.v_new_stride[i + 1];
+    }
+    w.slots = a.write_slots;
+    w.slot_dtype = a.write_slot_dtype;
+    w.num_tokens = (int64_t)a.batch * a.s_active;
+    w.k_cache = (void *)a.k_cache;
+    w.v_cache = (void *)a.v_cache;
+    w.cache_dtype = a.cache_dtype;
+    w.k_packed = a.k_packed;
+    for (int i = 0; i < 5; ++i) w.k_cache_stride[i] = a.k_cache_stride[i];
+    for (int i = 0; i < 4; ++i) w.v_cache_stride[i] = a.v_cache_stride[i];
+    w.num_blocks = a.num_blocks;
+    w.block_size = a.block_size;
+    w.num_kv_heads = a.num_kv_heads;
+    w.head_dim = a.head_dim;
+    w.quant_mode = a.quant_mode;
+    w.scale_per_head = a.quant_per_head;
+    w.k_scale = a.k_quant;
+    w.v_scale = a.v_quant;
+    return launch_kv_write(w, s);
+  }
+  const dim3 grid((unsigned)pl.grid);
+  if (a.split_event_begin) {
+    int rc = check_hip(hipEventRecord((hipEvent_t)a.split_event_begin, s),
+                       "decode: timing event");
+    if (rc) return rc;
+  }
+  if (pl.num_splits > 0 && kp.s_ctx - kp.S > 0) {
+    for (int cg = 0; cg < pl.col_groups; ++cg) {
+      kp.col0 = cg * 16;
+      const int ncp = std::min(16, pl.ncols - kp.col0);
+      if (a.head_dim == 128) {
+        if (a.k_packed) launch_split_ncp<128, true, true>(ncp, kp, grid, s);
+        else if (fp8) launch_split_ncp<128, true>(ncp, kp, grid, s);
+        else launch_split_ncp<128, false>(ncp, kp, grid, s);
+      } else {
+        if (a.k_packed) launch_split_ncp<64, true, true>(ncp, kp, grid, s);
+        else if (fp8) launch_split_ncp<64, true>(ncp, kp, grid, s);
+        else launch_split_ncp<64, false>(ncp, kp, grid, s);
+      }
+      int rc = check_hip(hipGetLastError(), "decode split launch");
+      if (rc) return rc;
+    }
+  }
+  if (a.split_event_end) {
+    int rc = check_hip(hipEventRecord((hipEvent_t)a.split_event_end, s),
+                       "decode: timing event");
+    if (rc) return rc;
+  }
   const int maxs = a.s_active <= 1 ? 1 : (a.s_active <= 4 ? 4 : kMaxAct);
   if (a.head_dim == 128) {
     if (maxs == 1) hipLaunchKernelGGL((decode_combine_kernel<128, 1>), cgrid, dim3(64), 0, s, cp);
