@@ -59,6 +59,10 @@ namespace mia {
 namespace {
 
 constexpr int kWaves = 4;
+// waves of a one-pass workgroup (one segment), two per SIMD (twelve at d =
+// 64 measured equal or slower: the per-wave chain of round trips, not the
+// tiles per wave, sets a short table's time)
+constexpr int one_waves(int) { return 8; }
 // occupancy the split kernel is compiled for: 2 workgroups per CU (8 waves,
 // 256 VGPRs each).  With streaming V loads an FP8 cache no longer needs a
 // third workgroup to keep HBM busy, and at 2 the FP8 kernels do not spill
@@ -341,9 +345,9 @@ MIA_DEV int wave_scan_incl(int x, int lane) {
 }
 
 // PK: the K cache is in the packed FP8 layout (FP8 only).  ONE: one-pass
-// mode (decode_onepass_kernel, P = CombineParams) for tables of at most
-// kOnePassTiles tiles: workgroup g takes segment (b, h) = (g / Hkv, g % Hkv),
-// its four waves stream contiguous runs of the segment's tiles, and the
+// mode (decode_onepass_kernel, P = CombineParams) for short tables:
+// workgroup g takes segment (b, h) = (g / Hkv, g % Hkv), its one_waves(D)
+// waves stream contiguous runs of the segment's tiles, and the
 // first wave merges their (m, l, o) through LDS, adds the active keys and
 // the sink, normalises and stores the bf16 output: no shares, no global
 // partials, no combine launch.
@@ -367,12 +371,13 @@ MIA_DEV void split_body(const P &c) {
   // V tile of each wave, bf16, rows of D elements, 16-byte chunks XOR-
   // swizzled by row (chunk c of token row t at c ^ (t % (D/8))): the writes
   // (16 lanes per row) and the transposed reads below are conflict-free
-  __shared__ __attribute__((aligned(16))) uint8_t v_lds[kWaves][kTile * D * 2];
+  constexpr int NW = ONE ? one_waves(D) : kWaves;  // waves per workgroup
+  __shared__ __attribute__((aligned(16))) uint8_t v_lds[NW][kTile * D * 2];
   __shared__ int s_R[kMaxRows + 1];
   __shared__ int s_lo[kMaxRows];
   __shared__ int s_hi[kMaxRows];
   __shared__ float s_minpos[kMaxRows];
-  __shared__ float s_one_m[kWaves][16], s_one_l[kWaves][16];  // one-pass merge
+  __shared__ float s_one_m[NW][16], s_one_l[NW][16];  // one-pass merge
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -639,8 +644,8 @@ MIA_DEV void split_body(const P &c) {
     // the segment's tiles dealt to the workgroup's waves in contiguous runs
     const int lo = readfirstlane(ri.lo), hi = readfirstlane(ri.hi);
     const int tf = lo / kTile, nt = hi > lo ? (hi + kTile - 1) / kTile - tf : 0;
-    const int r0 = tf + (nt * wave + kWaves - 1) / kWaves;
-    const int r1 = tf + (nt * (wave + 1) + kWaves - 1) / kWaves;
+    const int r0 = tf + (nt * wave + NW - 1) / NW;
+    const int r1 = tf + (nt * (wave + 1) + NW - 1) / NW;
     cur.t_lo = max(lo, r0 * kTile);
     cur.t_hi = max(cur.t_lo, min(hi, r1 * kTile));
     cur.next_x = 0;
@@ -822,13 +827,13 @@ MIA_DEV void split_body(const P &c) {
       if (wave != 0) return;
       float m = -INFINITY, l = 0.f;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) m = fmaxf(m, s_one_m[w][qcol]);
+      for (int w = 0; w < NW; ++w) m = fmaxf(m, s_one_m[w][qcol]);
       {
         const float mu = (m == -INFINITY) ? 0.f : m;
 #pragma unroll
         for (int blk = 0; blk < DB16; ++blk) oacc[blk] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) {
+        for (int w = 0; w < NW; ++w) {
           const float f = __builtin_amdgcn_exp2f(s_one_m[w][qcol] - mu);
           l += s_one_l[w][qcol] * f;
           const lds_u8_t *vwo = (lds_u8_t *)&v_lds[w][0];
@@ -934,7 +939,7 @@ __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(De
 }
 
 template <int D, int NCP, bool FP8, bool PK>
-__global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_onepass_kernel(CombineParams c) {
+__global__ __launch_bounds__(one_waves(D) * 64) void decode_onepass_kernel(CombineParams c) {
   split_body<D, NCP, FP8, PK, true>(c);
 }
 
@@ -1143,15 +1148,15 @@ void launch_split_ncp(int ncp, const DecodeKParams &kp, dim3 grid,
   else launch_split<D, 16, FP8, PK>(kp, grid, s);
 }
 
-// one-pass kernel: one four-wave workgroup per (row, kv head) segment
+// one-pass kernel: one workgroup of one_waves(D) waves per (row, kv head) segment
 template <int D, bool FP8, bool PK = false>
 void launch_onepass_ncp(int ncp, const CombineParams &cp, dim3 grid, hipStream_t s) {
   if (ncp <= 4)
-    hipLaunchKernelGGL((decode_onepass_kernel<D, 4, FP8, PK>), grid, dim3(kWaves * 64), 0, s, cp);
+    hipLaunchKernelGGL((decode_onepass_kernel<D, 4, FP8, PK>), grid, dim3(one_waves(D) * 64), 0, s, cp);
   else if (ncp <= 8)
-    hipLaunchKernelGGL((decode_onepass_kernel<D, 8, FP8, PK>), grid, dim3(kWaves * 64), 0, s, cp);
+    hipLaunchKernelGGL((decode_onepass_kernel<D, 8, FP8, PK>), grid, dim3(one_waves(D) * 64), 0, s, cp);
   else
-    hipLaunchKernelGGL((decode_onepass_kernel<D, 16, FP8, PK>), grid, dim3(kWaves * 64), 0, s, cp);
+    hipLaunchKernelGGL((decode_onepass_kernel<D, 16, FP8, PK>), grid, dim3(one_waves(D) * 64), 0, s, cp);
 }
 
 }  // namespace
@@ -1177,8 +1182,14 @@ int decode_noalloc_scratch(void **ptr) {
   return MIA_OK;
 }
 
-// tables of at most this many 32-token tiles take the one-pass kernel
+// one-pass kernel: tables of at most kOnePassTiles tiles (GPT-OSS 128-token
+// window: 13.6 against 21.7 us), or of at most kOnePassTilesFew when every
+// segment's workgroup fits on the device at once and no cache write follows
+// (Llama-3.2-1B, B=4, 1024 tokens: 16.5 against 17.7 us without a write;
+// with one the split path's combine writes the rows for free, 18.1 against
+// 18.5 us with the scatter launch after the one-pass kernel)
 constexpr int kOnePassTiles = 8;
+constexpr int kOnePassTilesFew = 32;
 
 DecodePlan plan_decode(const mia_decode_args &a) {
   DecodePlan pl;
@@ -1217,8 +1228,11 @@ DecodePlan plan_decode(const mia_decode_args &a) {
   const bool flat_new =
       a.batch <= 1 || (a.k_new_stride[0] == (int64_t)a.s_active * a.k_new_stride[1] &&
                        a.v_new_stride[0] == (int64_t)a.s_active * a.v_new_stride[1]);
-  pl.one_pass = a.split_tokens == 0 && t_max <= kOnePassTiles &&
-                (a.write_slots == nullptr || flat_new);
+  const bool short_tab =
+      t_max <= kOnePassTiles ||
+      (t_max <= kOnePassTilesFew && a.write_slots == nullptr &&
+       (int64_t)a.batch * a.num_kv_heads <= device_cu_count());
+  pl.one_pass = a.split_tokens == 0 && short_tab && (a.write_slots == nullptr || flat_new);
   const size_t rows = (size_t)a.batch * a.num_kv_heads * pl.num_splits * pl.ncols;
   size_t o_bytes = rows * (size_t)a.head_dim * sizeof(float);
   o_bytes = (o_bytes + 255) & ~(size_t)255;
