@@ -303,19 +303,36 @@ MIA_DEV uint3 ranked_tile(const PrefillKParams &p, int *scratch, int cap, SeqInf
   }
   __syncthreads();
   // rank of item j: items of higher cost, or of equal cost and lower index,
-  // counted 64 at a time with a ballot; each wave ranks every nw-th item
-  const uint32_t lane = tid & 63, wv = tid >> 6, nw = NT >> 6;
-  for (uint32_t j = wv; j < n_x; j += nw) {
-    const int cj = scratch[j];
+  // counted 64 at a time with a ballot; each wave ranks every nw-th item.
+  // The costs are read from LDS once (lane i holds items i, i + 64, ...,
+  // -1 past the items: costs are >= 0, and lane m the cost of the wave's
+  // m-th item) and the loop runs in scalar registers (wave-uniform bounds,
+  // v_readlane for the ranked item's cost); the chosen index is stored
+  // once, after the loop.
+  constexpr uint32_t kChunks = (kRankMax < NT ? kRankMax : NT) / 64;
+  const uint32_t lane = tid & 63, nw = NT >> 6;
+  const uint32_t wv = (uint32_t)readfirstlane((int)(tid >> 6));
+  const uint32_t nch = (n_x + 63) / 64;  // uniform
+  int cm[kChunks];
+#pragma unroll
+  for (uint32_t u = 0; u < kChunks; ++u)
+    cm[u] = (u < nch && 64 * u + lane < n_x) ? scratch[64 * u + lane] : -1;
+  // lane m holds the cost of the wave's m-th item (at most 64: n_x <= NT)
+  const int c_mine = wv + nw * lane < n_x ? scratch[wv + nw * lane] : 0;
+  const uint32_t n_mine = (n_x + nw - 1 - wv) / nw;
+  int found = -1;
+  for (uint32_t m = 0; m < n_mine; ++m) {
+    const uint32_t j = wv + nw * m;
+    const int cj = __builtin_amdgcn_readlane(c_mine, (int)m);
     uint32_t rank = 0;
-    for (uint32_t i0 = 0; i0 < n_x; i0 += 64) {
-      const uint32_t i = i0 + lane;
-      const int ci = i < n_x ? scratch[i] : -1;  // costs are >= 0
-      rank += (uint32_t)__builtin_popcountll(
-          __builtin_amdgcn_ballot_w64(ci > cj || (ci == cj && i < j)));
-    }
-    if (rank == k && lane == 0) scratch[n_x] = (int)j;
+#pragma unroll
+    for (uint32_t u = 0; u < kChunks; ++u)
+      if (u < nch)
+        rank += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(
+            cm[u] > cj || (cm[u] == cj && 64 * u + lane < j)));
+    if (rank == k) found = (int)j;
   }
+  if (found >= 0 && lane == 0) scratch[n_x] = found;
   __syncthreads();
   // LDS values are wave-uniform: kept in scalar registers
   const uint32_t jj = (uint32_t)readfirstlane(scratch[n_x]);
