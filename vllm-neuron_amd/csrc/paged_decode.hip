@@ -361,6 +361,7 @@ MIA_DEV void split_body(const P &c) {
   constexpr int DS = D / 8;            // lanes per V row (8 elems each)
   constexpr int TL = 64 / DS;          // V token lanes per wave
   constexpr int VPL = kTile / TL;      // V tokens per lane per tile
+  static_assert(16 % TL == 0, "a V load row group stays in one 16-token group");
   using KL = KLoad<FP8>;
   using raw_t = typename KL::raw_t;
   // K registers: 8 elements of one token, or for packed K 4 channels of
@@ -558,12 +559,13 @@ MIA_DEV void split_body(const P &c) {
   };
   // Blocks of the two 16-token groups of the tile at t0: a group (16
   // tokens, aligned) lies in one block as block_size % 16 == 0.  Loads are
-  // unconditional: every address is clamped into [t_lo, t_hi) of the piece
-  // (K per group, V per row of TL tokens; a clamped V row stays in its
-  // group's clamped block since TL divides 16), so it lies in an attended,
-  // allocated block, and rows outside the range are masked after the load
-  // (scores to -inf, V rows to zero).  A predicated load would make the
-  // compiler wait for each load before writing the zero of inactive lanes.
+  // unconditional: each group start is clamped into the groups of [t_lo,
+  // t_hi) of the piece, and K and V rows are read at their offset within
+  // that clamped group, so every row lies in an attended, allocated block.
+  // A group that needed the clamp lies wholly outside the piece, and rows
+  // outside the range are masked after the load (scores to -inf, V rows to
+  // zero).  A predicated load would make the compiler wait for each load
+  // before writing the zero of inactive lanes.
   struct TileRef {
     int tb[NSUB];  // clamped group start
     int bi[NSUB];  // its table entry
@@ -591,16 +593,19 @@ MIA_DEV void split_body(const P &c) {
         kr[st][ks] = k_load(kp + k_lane_off + ks * KSTEP_B);
     }
   };
+  // V row i * TL + tl of a tile: row (i * TL) % 16 + tl of group st; the
+  // group bases are computed once per tile and the rows step by a constant
+  const int64_t v_step = (int64_t)TL * p.vc_t * EB;
   auto issue_v = [&](raw_t (&vr)[VPL], const Item &it, const TileRef &r, int t0) {
-    const int v_first = (it.t_lo / TL) * TL, v_last = ((it.t_hi - 1) / TL) * TL;
+    (void)t0;
     const uint8_t *vbase = p.v_cache + (int64_t)it.h * p.vc_h * EB;
 #pragma unroll
-    for (int i = 0; i < VPL; ++i) {
-      const int st = (i * TL) / 16;
-      const int tb = min(max(t0 + i * TL, v_first), v_last);  // uniform
-      const uint8_t *vp = vbase + ((int64_t)r.phys[st] * p.vc_blk +
-                                   (int64_t)(tb - r.bi[st] * p.bs) * p.vc_t) * EB;
-      vr[i] = KL::load(vp + v_lane_off);
+    for (int st = 0; st < NSUB; ++st) {
+      const uint8_t *vg = vbase + ((int64_t)r.phys[st] * p.vc_blk +
+                                   (int64_t)(r.tb[st] - r.bi[st] * p.bs) * p.vc_t) * EB;
+#pragma unroll
+      for (int j = 0; j < 16 / TL; ++j)
+        vr[st * (16 / TL) + j] = KL::load(vg + j * v_step + v_lane_off);
     }
   };
   auto first_tile = [&](const Item &it) { return (it.t_lo / kTile) * kTile; };
@@ -716,40 +721,70 @@ MIA_DEV void split_body(const P &c) {
         for (int i = 0; i < 4; ++i) sc[st][i] = acc[i];
       }
       issue_k(kr, itN, rN);
+      // Scores outside the piece or masked become -inf.  The mask mode and
+      // window are uniform, so they are tested once per tile: per score
+      // they became a chain of branches on every tile.  A tile wholly inside
+      // the piece without a mask or window only drops padding columns.
+      if (p.mask_mode == 0 && !p.start) {
+        if (t0 >= cur.t_lo && t0 + kTile <= cur.t_hi) {
 #pragma unroll
-      for (int st = 0; st < NSUB; ++st) {
+          for (int st = 0; st < NSUB; ++st)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int tok = t0 + st * 16 + kg * 4 + i;
-          bool ok = col_ok && tok >= cur.t_lo && tok < cur.t_hi;
-          if (ok) {
-            if (p.mask_mode == 1) {
+            for (int i = 0; i < 4; ++i) sc[st][i] = col_ok ? sc[st][i] * scale2 : -INFINITY;
+        } else {
+#pragma unroll
+          for (int st = 0; st < NSUB; ++st)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int tok = t0 + st * 16 + kg * 4 + i;
+              const bool ok = col_ok && tok >= cur.t_lo && tok < cur.t_hi;
+              sc[st][i] = ok ? sc[st][i] * scale2 : -INFINITY;
+            }
+        }
+      } else if (p.mask_mode == 0) {
+#pragma unroll
+        for (int st = 0; st < NSUB; ++st)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int tok = t0 + st * 16 + kg * 4 + i;
+            const float ft = (float)tok;
+            const bool win = wrap_q ? (ft >= st_cur || ft < cur.minpos)
+                                    : (ft >= st_cur && ft < cur.minpos);
+            const bool ok = col_ok && tok >= cur.t_lo && tok < cur.t_hi && win;
+            sc[st][i] = ok ? sc[st][i] * scale2 : -INFINITY;
+          }
+      } else {
+#pragma unroll
+        for (int st = 0; st < NSUB; ++st)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int tok = t0 + st * 16 + kg * 4 + i;
+            bool ok = col_ok && tok >= cur.t_lo && tok < cur.t_hi;
+            if (ok) {
               const int hq = cur.h * p.G + g_q;
               const int64_t lin = seq_to_linear(tok, p.mask_bl);
               const int64_t mi = ((lin * p.B + cur.b) * p.Hq + hq) * p.S + s_q;
               ok = p.full_mask[mi] != 0.f;
-            } else if (p.start) {
-              const float ft = (float)tok;
-              ok = wrap_q ? (ft >= st_cur || ft < cur.minpos)
-                          : (ft >= st_cur && ft < cur.minpos);
             }
+            sc[st][i] = ok ? sc[st][i] * scale2 : -INFINITY;
           }
-          sc[st][i] = ok ? sc[st][i] * scale2 : -INFINITY;
-        }
       }
       // ---- V tile -> LDS (bf16; rows outside the item are zeroed: their
       // probabilities are 0 and the clamped loads hold other rows), then
       // the next tile's V loads
+      if (!(t0 >= cur.t_lo && t0 + kTile <= cur.t_hi)) {  // uniform: an edge tile
 #pragma unroll
-      for (int i = 0; i < VPL; ++i) {
-        const int tok = t0 + i * TL + tl;
-        const bool vok = tok >= cur.t_lo && tok < cur.t_hi;
-        raw_t rv = vr[i];
+        for (int i = 0; i < VPL; ++i) {
+          const int tok = t0 + i * TL + tl;
+          const bool vok = tok >= cur.t_lo && tok < cur.t_hi;
 #pragma unroll
-        for (int w = 0; w < (int)(sizeof(raw_t) / 4); ++w) rv[w] = vok ? rv[w] : 0u;
-        *(__attribute__((address_space(3))) u32x4_t *)(vw + v_wr_off(i)) =
-            __builtin_bit_cast(u32x4_t, KL::to_bf16(rv));
+          for (int w = 0; w < (int)(sizeof(raw_t) / 4); ++w) vr[i][w] = vok ? vr[i][w] : 0u;
+        }
       }
+#pragma unroll
+      for (int i = 0; i < VPL; ++i)
+        *(__attribute__((address_space(3))) u32x4_t *)(vw + v_wr_off(i)) =
+            __builtin_bit_cast(u32x4_t, KL::to_bf16(vr[i]));
       issue_v(vr, itN, rN, tN);
       // (every tile: cheap moves, and then no path leaves the landing loads
       // pending, so the compiler never waits on them elsewhere)
