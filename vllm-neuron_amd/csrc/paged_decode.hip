@@ -552,9 +552,15 @@ MIA_DEV void split_body(const P &c) {
   // wait for its in-flight K/V tiles.  Out-of-range ids are clamped.
   typedef const __attribute__((address_space(4))) int32_t const_i32_t;
   const_i32_t *const bt_s = (const_i32_t *)p.bt;
+  // Block and token strides in bytes, and table strides, below 2^31 (the
+  // host rejects larger ones): 32-bit scalars, where 64-bit strides held
+  // more scalar registers than the kernel has and spilled to vector lanes.
+  const uint32_t kblk_b = (uint32_t)p.kc_blk * EB, vblk_b = (uint32_t)p.vc_blk * EB;
+  const uint32_t kt_b = (uint32_t)p.kc_t * EB, vt_b = (uint32_t)p.vc_t * EB;
+  const uint32_t bt_b32 = (uint32_t)p.bt_b, bt_h32 = (uint32_t)p.bt_h, bt_j32 = (uint32_t)p.bt_j;
   auto block_at = [&](const Item &it, int bi) {
     const int j = min(bi, p.nblk - 1);
-    const int32_t v = bt_s[(int64_t)it.b * p.bt_b + (int64_t)it.h * p.bt_h + (int64_t)j * p.bt_j];
+    const int32_t v = bt_s[(uint32_t)it.b * bt_b32 + (uint32_t)it.h * bt_h32 + (uint32_t)j * bt_j32];
     return v < 0 ? 0 : (v >= p.nb ? p.nb - 1 : v);
   };
   // Blocks of the two 16-token groups of the tile at t0: a group (16
@@ -586,8 +592,8 @@ MIA_DEV void split_body(const P &c) {
     const uint8_t *kbase = p.k_cache + (int64_t)it.h * p.kc_h * EB;
 #pragma unroll
     for (int st = 0; st < NSUB; ++st) {
-      const uint8_t *kp = kbase + ((int64_t)r.phys[st] * p.kc_blk +
-                                   (int64_t)(r.tb[st] - r.bi[st] * p.bs) * p.kc_t) * EB;
+      const uint8_t *kp = kbase + (uint64_t)(uint32_t)r.phys[st] * kblk_b +
+                          (uint32_t)(r.tb[st] - r.bi[st] * p.bs) * kt_b;
 #pragma unroll
       for (int ks = 0; ks < KSTEPS; ++ks)
         kr[st][ks] = k_load(kp + k_lane_off + ks * KSTEP_B);
@@ -595,14 +601,14 @@ MIA_DEV void split_body(const P &c) {
   };
   // V row i * TL + tl of a tile: row (i * TL) % 16 + tl of group st; the
   // group bases are computed once per tile and the rows step by a constant
-  const int64_t v_step = (int64_t)TL * p.vc_t * EB;
+  const uint32_t v_step = TL * vt_b;
   auto issue_v = [&](raw_t (&vr)[VPL], const Item &it, const TileRef &r, int t0) {
     (void)t0;
     const uint8_t *vbase = p.v_cache + (int64_t)it.h * p.vc_h * EB;
 #pragma unroll
     for (int st = 0; st < NSUB; ++st) {
-      const uint8_t *vg = vbase + ((int64_t)r.phys[st] * p.vc_blk +
-                                   (int64_t)(r.tb[st] - r.bi[st] * p.bs) * p.vc_t) * EB;
+      const uint8_t *vg = vbase + (uint64_t)(uint32_t)r.phys[st] * vblk_b +
+                          (uint32_t)(r.tb[st] - r.bi[st] * p.bs) * vt_b;
 #pragma unroll
       for (int j = 0; j < 16 / TL; ++j)
         vr[st * (16 / TL) + j] = KL::load(vg + j * v_step + v_lane_off);
@@ -1323,6 +1329,19 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
   const int *cw = fp8 ? kClassWeightFp8 : kClassWeightBf16;
   for (int k = 0; k < 3; ++k) kp.cls_w[k] = cw[k];
   kp.nblk = a.blocks_per_seq;
+  {  // the split kernel forms cache and table offsets from 32-bit strides
+    const int64_t eb = fp8 ? 1 : 2, lim = (int64_t)1 << 31;
+    const int64_t bt_last = (int64_t)(a.batch - 1) * kp.bt_b + (int64_t)(a.num_kv_heads - 1) * kp.bt_h +
+                            (int64_t)(a.blocks_per_seq - 1) * kp.bt_j;
+    const bool ok = kp.kc_blk >= 0 && kp.vc_blk >= 0 && kp.kc_t >= 0 && kp.vc_t >= 0 &&
+                    kp.bt_b >= 0 && kp.bt_h >= 0 && kp.bt_j >= 0 && kp.kc_blk * eb < lim &&
+                    kp.vc_blk * eb < lim && kp.kc_t * eb * 2 * a.block_size < lim &&
+                    kp.vc_t * eb * a.block_size < lim && bt_last < lim;
+    if (!ok)
+      return set_error(MIA_ERR_VALUE,
+                       "paged decode: cache block or token strides of 2^31 bytes or more, or a "
+                       "block table of 2^31 entries or more");
+  }
   kp.num_splits = pl.num_splits;
   kp.nc_tot = pl.ncols;
   const size_t rows = (size_t)a.batch * a.num_kv_heads * pl.num_splits * pl.ncols;
