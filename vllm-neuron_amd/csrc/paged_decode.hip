@@ -368,6 +368,15 @@ MIA_DEV void split_body(const P &c) {
   // both tokens of the lane's pair (traded with the neighbour lane)
   using kraw_t = raw_t;
   constexpr int KSTEP_B = PK ? 64 : 32 * EB;  // bytes between k-steps of one lane
+  // An unpacked FP8 K row is read in 16-byte pieces: k-steps 2u and 2u + 1
+  // of lane group kg contract d = 64 u + 16 kg .. + 15, so one load fills
+  // two k-steps (the order of d in the dot product is free as long as Q
+  // follows it).  Other caches: k-step ks of group kg is d = 32 ks + 8 kg.
+  constexpr bool K16 = FP8 && !PK;
+  static_assert(!K16 || KSTEPS % 2 == 0, "k-steps pair up");
+  auto kd0 = [](int ks, int g) {  // first d of the 8 of (k-step, lane group)
+    return K16 ? (ks >> 1) * 64 + g * 16 + (ks & 1) * 8 : ks * 32 + g * 8;
+  };
 
   // V tile of each wave, bf16, rows of D elements, 16-byte chunks XOR-
   // swizzled by row (chunk c of token row t at c ^ (t % (D/8))): the writes
@@ -444,7 +453,7 @@ MIA_DEV void split_body(const P &c) {
   // parity k_odd loads channels 8 kg + 4 k_odd .. + 3 of both tokens
   const bool k_odd = qcol & 1;
   const int k_lane_off = PK ? (qcol & ~1) * (int)p.kc_t + kg * 16 + 8 * k_odd
-                            : (qcol * (int)p.kc_t + kg * 8) * EB;
+                            : (qcol * (int)p.kc_t + kg * (K16 ? 16 : 8)) * EB;
   const uint32_t k_sel_own = k_odd ? kPackedSelOdd : kPackedSelEven;
   const uint32_t k_sel_give = k_odd ? kPackedSelEven : kPackedSelOdd;
   auto k_bf16 = [&](const kraw_t &r) {
@@ -456,8 +465,9 @@ MIA_DEV void split_body(const P &c) {
   };
   const int v_lane_off = (tl * (int)p.vc_t + ds * 8) * EB;
   // K loads: streaming for bf16 (64 of a row's 256 bytes per load); an FP8
-  // row is read in 32-byte quarters by four loads, which stay plain so that
-  // the line is fetched once and served from L2 to the other three
+  // row is read in 64-byte halves (packed: 32-byte quarters) by several
+  // loads, which stay plain so that the line is fetched once and served from
+  // L2 to the others
   auto k_load = [&](const uint8_t *a) {
     if constexpr (FP8) return *reinterpret_cast<const kraw_t *>(a);
     else return stream_load<kraw_t>(a);
@@ -540,7 +550,7 @@ MIA_DEV void split_body(const P &c) {
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks)
       qf[ks] = __builtin_bit_cast(bf16x8_t,
-                                  *reinterpret_cast<const u32x4_t *>(qp + ks * 32 + kg * 8));
+                                  *reinterpret_cast<const u32x4_t *>(qp + kd0(ks, kg)));
   };
   auto load_start = [&](const Item &it) {
     return (p.mask_mode == 0 && p.start) ? p.start[(int64_t)it.b * p.S + s_q] : 0.f;
@@ -594,9 +604,18 @@ MIA_DEV void split_body(const P &c) {
     for (int st = 0; st < NSUB; ++st) {
       const uint8_t *kp = kbase + (uint64_t)(uint32_t)r.phys[st] * kblk_b +
                           (uint32_t)(r.tb[st] - r.bi[st] * p.bs) * kt_b;
+      if constexpr (K16) {
 #pragma unroll
-      for (int ks = 0; ks < KSTEPS; ++ks)
-        kr[st][ks] = k_load(kp + k_lane_off + ks * KSTEP_B);
+        for (int u = 0; u < KSTEPS / 2; ++u) {
+          const u32x4_t w = *reinterpret_cast<const u32x4_t *>(kp + k_lane_off + u * 64);
+          kr[st][2 * u] = kraw_t{w[0], w[1]};
+          kr[st][2 * u + 1] = kraw_t{w[2], w[3]};
+        }
+      } else {
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks)
+          kr[st][ks] = k_load(kp + k_lane_off + ks * KSTEP_B);
+      }
     }
   };
   // V row i * TL + tl of a tile: row (i * TL) % 16 + tl of group st; the
@@ -918,7 +937,7 @@ MIA_DEV void split_body(const P &c) {
           for (int e = 0; e < 8; ++e) {
             const float qv = __uint_as_float((e & 1) ? (qw[e >> 1] & 0xffff0000u) : (qw[e >> 1] << 16));
             const float kv = quant_roundtrip(
-                c, bf16_bits_to_f32(c.k_new[kb + ks * 32 + kg * 8 + e]), cur.h, c.k_quant);
+                c, bf16_bits_to_f32(c.k_new[kb + kd0(ks, kg) + e]), cur.h, c.k_quant);
             dot = fmaf(qv, kv, dot);
           }
         }
