@@ -358,7 +358,9 @@ MIA_DEV void split_body(const P &c) {
   constexpr int EB = FP8 ? 1 : 2;      // cache element bytes
   constexpr int KSTEPS = D / 32;
   constexpr int NSUB = kTile / 16;
-  constexpr int DS = D / 8;            // lanes per V row (8 elems each)
+  constexpr int VE = FP8 ? 16 : 8;     // V elements per lane per load (16 bytes)
+  constexpr int VCH = VE / 8;          // 16-byte bf16 LDS chunks per V load
+  constexpr int DS = D / VE;           // lanes per V row
   constexpr int TL = 64 / DS;          // V token lanes per wave
   constexpr int VPL = kTile / TL;      // V tokens per lane per tile
   static_assert(16 % TL == 0, "a V load row group stays in one 16-token group");
@@ -463,7 +465,7 @@ MIA_DEV void split_body(const P &c) {
     else
       return KL::to_bf16(r);
   };
-  const int v_lane_off = (tl * (int)p.vc_t + ds * 8) * EB;
+  const int v_lane_off = (tl * (int)p.vc_t + ds * VE) * EB;
   // K loads: streaming for bf16 (64 of a row's 256 bytes per load); an FP8
   // row is read in 64-byte halves (packed: 32-byte quarters) by several
   // loads, which stay plain so that the line is fetched once and served from
@@ -497,11 +499,11 @@ MIA_DEV void split_body(const P &c) {
   for (int blk = 0; blk < DB16; ++blk)
     v_rd_off[blk] = tr_row * VROWB + ((((blk * 2 + ((tr_s >> 1) & 1)) ^ tr_x)) << 4) +
                     ((tr_s & 1) << 3);
-  // row of V load i of this lane: i * TL + tl; its swizzle repeats every
-  // VNCH / TL loads
-  auto v_wr_off = [&](int i) {
+  // row of V load i of this lane: i * TL + tl; bf16 chunk h of the load is
+  // chunk ds * VCH + h of the row, XOR-swizzled by the row
+  auto v_wr_off = [&](int i, int h) {
     const int t = i * TL + tl;
-    return (uint32_t)(t * VROWB + ((ds ^ (t & (VNCH - 1))) << 4));
+    return (uint32_t)(t * VROWB + (((ds * VCH + h) ^ (t & (VNCH - 1))) << 4));
   };
 
   // The piece of this wave starting at flattened tile x (x < x_end): its
@@ -621,7 +623,7 @@ MIA_DEV void split_body(const P &c) {
   // V row i * TL + tl of a tile: row (i * TL) % 16 + tl of group st; the
   // group bases are computed once per tile and the rows step by a constant
   const uint32_t v_step = TL * vt_b;
-  auto issue_v = [&](raw_t (&vr)[VPL], const Item &it, const TileRef &r, int t0) {
+  auto issue_v = [&](u32x4_t (&vr)[VPL], const Item &it, const TileRef &r, int t0) {
     (void)t0;
     const uint8_t *vbase = p.v_cache + (int64_t)it.h * p.vc_h * EB;
 #pragma unroll
@@ -630,7 +632,7 @@ MIA_DEV void split_body(const P &c) {
                           (uint32_t)(r.tb[st] - r.bi[st] * p.bs) * vt_b;
 #pragma unroll
       for (int j = 0; j < 16 / TL; ++j)
-        vr[st * (16 / TL) + j] = KL::load(vg + j * v_step + v_lane_off);
+        vr[st * (16 / TL) + j] = stream_load<u32x4_t>(vg + j * v_step + v_lane_off);
     }
   };
   auto first_tile = [&](const Item &it) { return (it.t_lo / kTile) * kTile; };
@@ -695,7 +697,7 @@ MIA_DEV void split_body(const P &c) {
   bf16x8_t q_hold[KSTEPS];
   float st_hold = 0.f, kdq_hold = 1.f;
   kraw_t kr[NSUB][KSTEPS];
-  raw_t vr[VPL];
+  u32x4_t vr[VPL];
   if (!ONE || cur.t_lo < cur.t_hi) {  // a one-pass row may have no prior key
     const TileRef r0 = tile_ref(cur, first_tile(cur));
     issue_k(kr, cur, r0);
@@ -803,13 +805,19 @@ MIA_DEV void split_body(const P &c) {
           const int tok = t0 + i * TL + tl;
           const bool vok = tok >= cur.t_lo && tok < cur.t_hi;
 #pragma unroll
-          for (int w = 0; w < (int)(sizeof(raw_t) / 4); ++w) vr[i][w] = vok ? vr[i][w] : 0u;
+          for (int w = 0; w < 4; ++w) vr[i][w] = vok ? vr[i][w] : 0u;
         }
       }
+      typedef __attribute__((address_space(3))) u32x4_t lds_u32x4_t;
 #pragma unroll
-      for (int i = 0; i < VPL; ++i)
-        *(__attribute__((address_space(3))) u32x4_t *)(vw + v_wr_off(i)) =
-            __builtin_bit_cast(u32x4_t, KL::to_bf16(vr[i]));
+      for (int i = 0; i < VPL; ++i) {
+        if constexpr (FP8) {
+          *(lds_u32x4_t *)(vw + v_wr_off(i, 0)) = e4m3fn_x8_to_bf16_scaled(u32x2_t{vr[i][0], vr[i][1]});
+          *(lds_u32x4_t *)(vw + v_wr_off(i, 1)) = e4m3fn_x8_to_bf16_scaled(u32x2_t{vr[i][2], vr[i][3]});
+        } else {
+          *(lds_u32x4_t *)(vw + v_wr_off(i, 0)) = vr[i];
+        }
+      }
       issue_v(vr, itN, rN, tN);
       // (every tile: cheap moves, and then no path leaves the landing loads
       // pending, so the compiler never waits on them elsewhere)
