@@ -369,15 +369,17 @@ MIA_DEV void split_body(const P &c) {
   // K registers: 8 elements of one token, or for packed K 4 channels of
   // both tokens of the lane's pair (traded with the neighbour lane)
   using kraw_t = raw_t;
-  constexpr int KSTEP_B = PK ? 64 : 32 * EB;  // bytes between k-steps of one lane
-  // An unpacked FP8 K row is read in 16-byte pieces: k-steps 2u and 2u + 1
-  // of lane group kg contract d = 64 u + 16 kg .. + 15, so one load fills
-  // two k-steps (the order of d in the dot product is free as long as Q
-  // follows it).  Other caches: k-step ks of group kg is d = 32 ks + 8 kg.
+  constexpr int KSTEP_B = 32 * EB;  // bytes between k-steps of one lane (bf16)
+  // An FP8 K row is contracted in the order where k-steps 2u and 2u + 1 of
+  // lane group kg take d = 64 u + 16 kg .. + 15, so that one 16-byte load
+  // of an unpacked row fills two k-steps (the order of d in the dot product
+  // is free as long as Q follows it; the packed layout reads the same d so
+  // both layouts give identical results).  A bf16 cache: k-step ks of group
+  // kg is d = 32 ks + 8 kg.
   constexpr bool K16 = FP8 && !PK;
-  static_assert(!K16 || KSTEPS % 2 == 0, "k-steps pair up");
+  static_assert(!FP8 || KSTEPS % 2 == 0, "k-steps pair up");
   auto kd0 = [](int ks, int g) {  // first d of the 8 of (k-step, lane group)
-    return K16 ? (ks >> 1) * 64 + g * 16 + (ks & 1) * 8 : ks * 32 + g * 8;
+    return FP8 ? (ks >> 1) * 64 + g * 16 + (ks & 1) * 8 : ks * 32 + g * 8;
   };
 
   // V tile of each wave, bf16, rows of D elements, 16-byte chunks XOR-
@@ -454,7 +456,7 @@ MIA_DEV void split_body(const P &c) {
   // packed K: token pair (qcol & ~1) at its even token's offset; lane
   // parity k_odd loads channels 8 kg + 4 k_odd .. + 3 of both tokens
   const bool k_odd = qcol & 1;
-  const int k_lane_off = PK ? (qcol & ~1) * (int)p.kc_t + kg * 16 + 8 * k_odd
+  const int k_lane_off = PK ? (qcol & ~1) * (int)p.kc_t + kg * 32 + 8 * k_odd
                             : (qcol * (int)p.kc_t + kg * (K16 ? 16 : 8)) * EB;
   const uint32_t k_sel_own = k_odd ? kPackedSelOdd : kPackedSelEven;
   const uint32_t k_sel_give = k_odd ? kPackedSelEven : kPackedSelOdd;
@@ -615,8 +617,8 @@ MIA_DEV void split_body(const P &c) {
         }
       } else {
 #pragma unroll
-        for (int ks = 0; ks < KSTEPS; ++ks)
-          kr[st][ks] = k_load(kp + k_lane_off + ks * KSTEP_B);
+        for (int ks = 0; ks < KSTEPS; ++ks)  // packed: byte 2 d of the pair row
+          kr[st][ks] = k_load(kp + k_lane_off + (PK ? 2 * kd0(ks, 0) : ks * KSTEP_B));
       }
     }
   };
