@@ -397,3 +397,21 @@ def test_one_pass_full_mask_mode(gpu):
     # row's position, so the tiles are dealt to the waves differently and
     # the merge order differs: one bf16 step at |o| < 2
     assert (out.float() - base.float()).abs().max().item() <= 8e-3
+
+
+def test_decode_rejects_table_offsets_past_2_31(gpu):
+    """The split kernel forms block-table offsets in 32 bits: a table whose
+    last row starts 2^31 entries after its first is rejected before any
+    launch.  The table is a real view of a 16 GiB allocation, so even a
+    launch would read only allocated memory."""
+    cfg = _small_cfg(**CASES[1])
+    b = _make(cfg, gpu)
+    B, nblk = b.block_table.shape[0], b.block_table.shape[-1]
+    assert B >= 2 and b.block_table.dim() == 2
+    wide = torch.empty((B, (1 << 31) + 64), dtype=b.block_table.dtype, device=gpu)
+    wide[:, :nblk] = b.block_table
+    b.block_table = wide[:, :nblk]
+    with pytest.raises(ValueError, match="2\\^31"):
+        _run_core(b)
+    del wide
+    torch.cuda.empty_cache()
