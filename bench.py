@@ -21,7 +21,9 @@ The same line carries
     chunk, Llama-3-8B mixed batch) in µs per call from HIP graph replays,
     each with its algorithmic rate and roofline fraction;
   * ``cpu_baseline``: the CPU restatement of the reference's torch decode
-    path on a bounded sample of the same workload, timed on this host.
+    path on a bounded sample of the same workload, timed on this host; the
+    prefill leg and every secondary workload carry the CPU time of their
+    restated reference calls beside the GPU time (decode rows sampled).
 """
 from __future__ import annotations
 
@@ -140,7 +142,7 @@ def bench_prefill(dev, steps, warmup):
         times.append(e0.elapsed_time(e1) / steps)
     flops = W.prefill_flops(b)
     ms = statistics.median(times)
-    return dict(flops=flops, ms=ms, ms_med=ms, tflops=flops / (ms * 1e-3) / 1e12)
+    return dict(flops=flops, ms=ms, ms_med=ms, tflops=flops / (ms * 1e-3) / 1e12, batch=b)
 
 
 def _graph_us(fn, dev, reps: int, per_graph: int = 8) -> float:
@@ -172,14 +174,15 @@ def _graph_us(fn, dev, reps: int, per_graph: int = 8) -> float:
     return e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
 
 
-def bench_secondary(dev, reps: int) -> dict:
+def bench_secondary(dev, reps: int, cpu_rows: int = 0) -> dict:
     """The other benchmark workloads, each as µs per call (HIP graph replay)
     with its algorithmic rate and roofline fraction: GPT-OSS-120B-shaped
     decode (full-attention and 128-token sliding-window layers, sinks), the
     long-context FP8 decode, the Llama-3.2-1B decode, the 2048-token FP8
     prefill chunk, and the Llama-3-8B mixed batch (4 x 512 chunked prefill +
     60 decode rows) as one call against max(bytes / HBM peak, FLOPs / bf16
-    peak)."""
+    peak).  With ``cpu_rows`` each entry also carries the CPU time of the
+    restated reference path for the same call (decode rows sampled)."""
     import torch
 
     from vllm_neuron_amd import _kernels as K
@@ -216,6 +219,8 @@ def bench_secondary(dev, reps: int) -> dict:
             rec.update(bound="hbm", frac=round(gbs / HBM_PEAK_GBS, 4))
         else:
             rec.update(bound="latency")
+        if cpu_rows:
+            rec.update(_cpu_secondary(name, b, cpu_rows))
         out[name] = rec
         del b, ws
     for name in ("fp8_prefill_2048",):
@@ -236,6 +241,8 @@ def bench_secondary(dev, reps: int) -> dict:
         tf = fl / (us * 1e-6) / 1e12
         out[name] = {"us_per_call": round(us, 2), "flops": fl, "tflops": round(tf, 1),
                      "bound": "mfma", "frac": round(tf / BF16_PEAK_TFLOPS, 4)}
+        if cpu_rows:
+            out[name].update(_cpu_secondary(name, b, cpu_rows))
         del b
     m = W.make_mixed_batch(dev)
     db, pb = m.decode, m.prefill
@@ -260,6 +267,9 @@ def bench_secondary(dev, reps: int) -> dict:
         "floor_us": round(floor_us, 1), "frac_of_floor": round(floor_us / us, 4),
         "dominant": "hbm" if nbytes / (HBM_PEAK_GBS * 1e9) >= fl / (BF16_PEAK_TFLOPS * 1e12)
         else "mfma"}
+    if cpu_rows:
+        out["llama3_8b_mixed_4x512_plus_60_decode"].update(
+            _cpu_secondary("llama3_8b_mixed", m, cpu_rows))
     return out
 
 
@@ -274,6 +284,119 @@ def _cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+def _cpu_threads() -> int:
+    import torch
+
+    threads = int(os.environ.get("OMP_NUM_THREADS", 0)) or (os.cpu_count() or 1)
+    torch.set_num_threads(threads)
+    return torch.get_num_threads()
+
+
+def _cpu_median_s(fn, reps: int = 3) -> float:
+    """Median wall time of ``fn()`` over ``reps`` runs after one warm-up."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts)
+
+
+def _cpu_decode_call(gb, rows: int):
+    """One call of the oracle's restatement of the reference torch decode
+    path (attention_decode.py:653-1182; the mask pre-generated as the
+    callers do) on the first ``rows`` rows of decode batch ``gb``, copied to
+    host memory with the cache blocks those rows read (block 0 = null).
+    FP8 caches with per-kv-head scales run the reference's scalar-scale
+    semantics once per kv head (heads are independent).  Returns a
+    zero-argument callable and the row count used."""
+    import torch
+
+    from oracle import decode as OD
+    from oracle import mask as OM
+
+    cfg = gb.cfg
+    B, Hq, Hkv, d, bs = cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.block_size
+    R = min(rows, B)
+    G = Hq // Hkv
+    table = gb.block_table[:R].cpu()
+    used = torch.unique(table[table >= 0])
+    remap = torch.full((gb.k_cache.shape[0],), -1, dtype=torch.int32)
+    remap[used.long()] = torch.arange(1, used.numel() + 1, dtype=torch.int32)
+    t2 = torch.where(table >= 0, remap[table.clamp_min(0).long()], table)
+    idx = torch.cat([torch.zeros(1, dtype=torch.long), used.long()]).to(gb.k_cache.device)
+    kc, vc = gb.k_cache[idx].cpu(), gb.v_cache[idx].cpu()
+    S_ctx = table.shape[1] * bs
+    pos = gb.pos[:R].cpu()
+    start = None if gb.start is None else gb.start[:R].cpu().reshape(1, -1)
+    scale = d ** -0.5
+    q, kn, vn = (t[:R].cpu() for t in (gb.q, gb.k_new, gb.v_new))
+    sink = None if gb.sink is None else gb.sink.cpu().reshape(-1, 1)
+    if not cfg.fp8:
+        X = torch.cat([q.reshape(R, 1, -1), kn.reshape(R, 1, -1), vn.reshape(R, 1, -1)], -1)
+        Wq = torch.eye(X.shape[-1], dtype=torch.bfloat16)
+        mask = OM.gen_mask_torch(pos.reshape(1, -1), R, Hq, 1, S_ctx, start_pos=start,
+                                 block_len=bs)
+        return (lambda: OD.ref_attention_decode(X, Wq, kc, vc, t2, mask, sink=sink,
+                                                softmax_scale=scale)), R
+    mask = OM.gen_mask_torch(pos.reshape(1, -1), R, G, 1, S_ctx, start_pos=start, block_len=bs)
+    per_head = []
+    for h in range(Hkv):
+        X = torch.cat([q[:, :, h * G:(h + 1) * G].reshape(R, 1, -1), kn[:, :, h], vn[:, :, h]],
+                      -1)
+        per_head.append((X, torch.eye(X.shape[-1], dtype=torch.bfloat16),
+                         kc[:, h:h + 1].contiguous(), vc[:, h:h + 1].contiguous(),
+                         gb.k_quant[h].cpu().view(1, 1), gb.v_quant[h].cpu().view(1, 1),
+                         scale * float(gb.k_dequant[h])))
+
+    def call():
+        for X, Wq, kch, vch, rk, rv, sc in per_head:
+            OD.ref_attention_decode(X, Wq, kch, vch, t2, mask, softmax_scale=sc, k_scale=rk,
+                                    v_scale=rv)
+    return call, R
+
+
+def _cpu_prefill_call(pb, k_cache=None, v_cache=None):
+    """The oracle's restatement of the reference torch segmented path
+    (attention_segmented_cte.py:122-246), one call per sequence as the
+    reference runs it, over every sequence of prefill batch ``pb`` (cache
+    already holding the new rows).  FP8 caches with per-kv-head scales run
+    once per kv head with that head's scale folded into ``scale`` and the
+    output, as the reference's callers fold a scalar one
+    (gpt_oss/model_bf16.py:699-727)."""
+    import torch
+
+    from oracle import segmented as OSg
+
+    cfg = pb.cfg
+    kc = (pb.k_cache if k_cache is None else k_cache).cpu()
+    vc = (pb.v_cache if v_cache is None else v_cache).cpu()
+    Hkv, G = cfg.kv_heads, cfg.q_heads // cfg.kv_heads
+    scale = cfg.head_dim ** -0.5
+    cu = pb.cu_seqlens.cpu().tolist()
+    prior = pb.prior.cpu()
+    seqs = []
+    for i in range(len(cu) - 1):
+        q = pb.q[cu[i]:cu[i + 1]].cpu().transpose(0, 1).contiguous()   # [Hq, S_q, D]
+        seqs.append((q, pb.block_table[i:i + 1].cpu(), prior[i:i + 1].view(1, 1)))
+    if not cfg.fp8:
+        def call():
+            for q, tab, pr in seqs:
+                OSg.ref_segmented_attention(q, kc, vc, tab, pr, cfg.block_size, scale)
+        return call
+    kh = [(kc[:, h:h + 1].contiguous(), vc[:, h:h + 1].contiguous(),
+           scale * float(pb.k_dequant[h]), float(pb.v_dequant[h])) for h in range(Hkv)]
+
+    def call_fp8():
+        for q, tab, pr in seqs:
+            for h, (kch, vch, sc, vd) in enumerate(kh):
+                o = OSg.ref_segmented_attention(q[h * G:(h + 1) * G], kch, vch, tab, pr,
+                                                cfg.block_size, sc)
+                o.float().mul_(vd)
+    return call_fp8
+
+
 def cpu_baseline(gpu_batch, rows=16):
     """The oracle (CPU restatement of the reference torch decode path,
     attention_decode.py:653-1182, mask pre-generated as the Llama caller
@@ -282,41 +405,64 @@ def cpu_baseline(gpu_batch, rows=16):
     of the sampled rows (same formula as the GPU line)."""
     import torch
 
-    from oracle import decode as OD
-    from oracle import mask as OM
-
-    threads = int(os.environ.get("OMP_NUM_THREADS", 0)) or (os.cpu_count() or 1)
-    torch.set_num_threads(threads)
+    threads = _cpu_threads()
     cfg = gpu_batch.cfg
     B, Hq, Hkv, d, bs = cfg.batch, cfg.q_heads, cfg.kv_heads, cfg.head_dim, cfg.block_size
-    rows = min(rows, B)
-    kc, vc = gpu_batch.k_cache.cpu(), gpu_batch.v_cache.cpu()
-    q, kn, vn = (t[:rows].cpu() for t in (gpu_batch.q, gpu_batch.k_new, gpu_batch.v_new))
-    table = gpu_batch.block_table[:rows].cpu()
-    pos = gpu_batch.pos[:rows].cpu()
-    S_ctx = table.shape[1] * bs
-    X = torch.cat([q.reshape(rows, 1, -1), kn.reshape(rows, 1, -1), vn.reshape(rows, 1, -1)], -1)
-    Wq = torch.eye(X.shape[-1], dtype=torch.bfloat16)
-    mask = OM.gen_mask_torch(pos.reshape(1, -1), rows, Hq, 1, S_ctx, block_len=bs)
-    times = []
-    for _ in range(4):  # 1 warm-up + median of 3
-        t0 = time.perf_counter()
-        OD.ref_attention_decode(X, Wq, kc, vc, table, mask)
-        times.append(time.perf_counter() - t0)
-    t = statistics.median(times[1:])
+    call, rows = _cpu_decode_call(gpu_batch, rows)
+    t = _cpu_median_s(call)
     L = gpu_batch.ctx[:rows].cpu().to(torch.int64)
     nbytes = (int(L.sum()) * Hkv * d * 2 * 2 + rows * Hq * d * 2 * 2
               + rows * Hkv * d * 2 * 2 + int(((L + bs - 1) // bs).sum()) * 4)
     return {
         "value": round(nbytes / t / 1e9, 4),
         "unit": "GB/s",
-        "cores": torch.get_num_threads(),
+        "cores": threads,
         "cpu_model": _cpu_model(),
         "kind": "port",
         "sample": (f"first {rows} of {B} batch rows of the Llama-3-8B decode batch; "
                    f"{t * 1e3:.1f} ms per call, median of 3 after 1 warm-up; "
                    "restated reference torch decode path (bf16, pre-generated mask)"),
     }
+
+
+def cpu_prefill_baseline(pb, flops: int) -> dict:
+    """The restated reference segmented path over the 4 x 512 sub-batch
+    (one call per sequence), timed on this host."""
+    threads = _cpu_threads()
+    t = _cpu_median_s(_cpu_prefill_call(pb))
+    return {"us_per_call": round(t * 1e6, 1), "tflops": round(flops / t / 1e12, 5),
+            "cores": threads, "cpu_model": _cpu_model(), "kind": "port",
+            "sample": "the whole sub-batch: one restated reference segmented call per "
+                      "sequence (fp32), median of 3 after 1 warm-up"}
+
+
+def _cpu_secondary(name: str, obj, rows: int) -> dict:
+    """CPU time of one secondary workload's restated reference call (decode
+    rows sampled, prefill whole), on this host."""
+    threads = _cpu_threads()
+    if name.startswith("llama3_8b_mixed"):
+        m = obj
+        dcall, R = _cpu_decode_call(m.decode, rows)
+        pcall = _cpu_prefill_call(m.prefill, m.k_cache, m.v_cache)
+        td = _cpu_median_s(dcall)
+        tp = _cpu_median_s(pcall)
+        Bd = m.decode.cfg.batch
+        return {"cpu_us_per_call": round((tp + td * Bd / R) * 1e6, 1),
+                "cpu_sample": (f"prefill: 4 segmented calls (whole, {tp * 1e6:.0f} us); decode: "
+                               f"first {R} of {Bd} rows ({td * 1e6:.0f} us), scaled linearly "
+                               f"to {Bd} rows"),
+                "cpu_cores": threads}
+    if hasattr(obj, "cu_seqlens"):
+        t = _cpu_median_s(_cpu_prefill_call(obj))
+        return {"cpu_us_per_call": round(t * 1e6, 1), "cpu_sample": "whole call",
+                "cpu_cores": threads}
+    call, R = _cpu_decode_call(obj, rows)
+    t = _cpu_median_s(call)
+    B = obj.cfg.batch
+    rec = {"cpu_us_per_call": round(t * B / R * 1e6, 1), "cpu_cores": threads}
+    rec["cpu_sample"] = ("whole batch" if R == B else
+                         f"first {R} of {B} rows ({t * 1e6:.0f} us), scaled linearly to {B}")
+    return rec
 
 
 def _measured_traffic(kernel: str, workload: str):
@@ -494,9 +640,11 @@ def main() -> int:
         },
     }
     if not args.no_secondary:
-        line["secondary"] = bench_secondary(dev, max(4, args.steps // 8))
+        line["secondary"] = bench_secondary(dev, max(4, args.steps // 8),
+                                            0 if args.no_cpu_baseline else args.cpu_rows)
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(dec["batch"], args.cpu_rows)
+        line["prefill"]["cpu_baseline"] = cpu_prefill_baseline(pre["batch"], pre["flops"])
     else:
         line["cpu_baseline"] = None
     print(json.dumps(line), flush=True)

@@ -481,6 +481,12 @@ typedef struct {
   int32_t out_rows;        /* >= prior_rows + rows */
   int32_t head_dim;
   int32_t out_dim;         /* multiple of 8, head_dim <= out_dim <= 128 */
+  /* Optional device int32 [1]: the prior row count read at run time, so
+   * that a caller under graph capture or torch.compile never reads it on the
+   * host (attention_cte.py:96-118 slices k_prior[:, :prior_used_len]).  When
+   * non-NULL, P = clamp(*prior_rows_dev, 0, prior_rows) and prior_rows is
+   * the capacity of `prior`; rows [P + rows, out_rows) are zero. */
+  const int32_t *prior_rows_dev;
 } mia_stage_args;
 
 int mia_stage_rows(const mia_stage_args *args, mia_stream_t stream);

@@ -295,3 +295,15 @@ def test_noalloc_decode_rejects_plans_beyond_its_static_scratch():
         N.check(L.mia_paged_decode_noalloc(ctypes.byref(a), None), "paged_decode_noalloc")
     hdr = (ROOT / "include" / "mia_attn.h").read_text()
     assert f"MIA_DECODE_NOALLOC_SCRATCH_BYTES ({N.DECODE_NOALLOC_SCRATCH_BYTES >> 20}u << 20)" in hdr
+
+
+def test_one_pass_plan_needs_no_split_scratch():
+    """A short table (one-pass kernel: partials in LDS) reports a token
+    workspace size however large its split-K layout would be, so the
+    allocation-free entry point does not refuse it (batch 1024, 16 query
+    columns: the split layout would need ~600 MB)."""
+    L = N.lib()
+    a = _decode_args(batch=1024, blocks_per_seq=8, s_active=2, num_q_heads=64, num_kv_heads=8)
+    assert 0 < L.mia_decode_workspace_bytes(ctypes.byref(a)) <= 4096
+    big = _decode_args(batch=1024, blocks_per_seq=16, s_active=2, num_q_heads=64, num_kv_heads=8)
+    assert L.mia_decode_workspace_bytes(ctypes.byref(big)) > N.DECODE_NOALLOC_SCRATCH_BYTES

@@ -1,12 +1,18 @@
-"""The drop-in under the reference callers' execution modes, on the GPU:
+"""The drop-ins under the reference callers' execution modes, on the GPU:
 
 * ``torch.compile(fullgraph=True)`` (AOT autograd with functionalization,
   no code generation) of the fused decode (stages 1-8 with the in-place
-  cache update) and of the segmented prefill gives outputs and cache bytes
-  equal bit for bit to eager execution;
+  cache update), the segmented prefill, the dense ``flash_attention`` with
+  a prefix and a context-parallel offset, the fused SWA layer (bf16 and
+  packed FP8 caches) and ``qkv_proj`` with its cache write gives outputs
+  and cache bytes equal bit for bit to eager execution;
 * a HIP graph capturing the decode (with its fused cache write) and the
   prefill replays several times, with unrelated eager work and host
   synchronisation between replays, each replay equal to the eager result;
+  graphs of the other drop-ins replay equal to eager calls after the
+  device scalars they read (prior length, prior_used_len, cp_offset) are
+  changed between replays, which shows that none was read on the host at
+  capture;
 * ``torch.library.opcheck`` accepts the registered ops (schema mutation
   annotations, fake implementations, dispatch under AOT).
 """
@@ -18,6 +24,7 @@ from vllm_neuron_amd import workloads as W
 from vllm_neuron_amd.functional.attention.attention_decode import (
     attention_decode, paged_decode_core)
 from vllm_neuron_amd.functional.attention.attention_segmented_cte import segmented_attention
+from vllm_neuron_amd.functional import flash_attention, qkv_proj, swa_fused_attention
 
 pytestmark = pytest.mark.gpu
 
@@ -122,10 +129,11 @@ def test_opcheck_registered_ops(gpu):
     b = W.make_decode_batch(cfg, gpu)
     out = torch.empty_like(b.q)
     slots = b.slots.reshape(-1).contiguous()
-    torch.library.opcheck(
-        torch.ops.mia.paged_decode.default,
-        (b.q, b.k_new, b.v_new, b.k_cache, b.v_cache, b.block_table, out, None, b.pos, None,
-         None, None, None, None, None, None, None, slots, 0.125, 0, 0, False, 0, False, False))
+    common = (b.q, b.k_new, b.v_new, b.k_cache, b.v_cache, b.block_table, out, None, b.pos, None,
+              None, None, None, None, None, None, None)
+    scal = (0.125, 0, 0, False, 0, False, False)
+    torch.library.opcheck(torch.ops.mia.paged_decode.default, (*common, *scal))
+    torch.library.opcheck(torch.ops.mia.paged_decode_write.default, (*common, slots, *scal))
     pcfg = W.PrefillConfig("t", 1, 8, 2, 64, 16, 40, 32, 32, seed=5)
     pb = W.make_prefill_batch(pcfg, gpu)
     pout = torch.empty_like(pb.q)
@@ -137,3 +145,175 @@ def test_opcheck_registered_ops(gpu):
     torch.library.opcheck(
         torch.ops.mia.kv_write.default,
         (pb.k_new, pb.v_new, pb.slots, pb.k_cache, pb.v_cache, False, 0, None, None, False))
+    src = torch.randn(2, 40, 80, device=gpu).to(torch.bfloat16)
+    prior = torch.randn(2, 24, 80, device=gpu).to(torch.bfloat16)
+    torch.library.opcheck(torch.ops.mia.stage_rows.default,
+                          (src, prior, torch.tensor([17], dtype=torch.int32, device=gpu), 24,
+                           128, 128))
+
+
+# ---------------------------------------------------------------------------
+# the other drop-ins: compiled and graph-replayed, against eager
+# ---------------------------------------------------------------------------
+def _compiled(fn):
+    torch._dynamo.reset()
+    return torch.compile(fn, fullgraph=True, backend="aot_eager")
+
+
+def _fa_inputs(dev, seed=21):
+    g = torch.Generator().manual_seed(seed)
+    B, B_kv, S, D, Pc = 8, 2, 200, 128, 150
+    r = lambda *sh: torch.randn(*sh, generator=g).to(torch.bfloat16).to(dev)
+    return dict(q=r(B, S, D), k=r(B_kv, D, S), v=r(B_kv, S, D), k_prior=r(B_kv, D, Pc),
+                v_prior=r(B_kv, Pc, D), sink=torch.randn(B, 1, generator=g).to(dev),
+                prior_used_len=torch.tensor([97], dtype=torch.int32, device=dev),
+                cp_offset=torch.tensor([[5]], dtype=torch.int32, device=dev))
+
+
+def _fa(q, k, v, k_prior, v_prior, sink, prior_used_len, cp_offset):
+    return flash_attention(q, k, v, k_prior=k_prior, v_prior=v_prior, sink=sink,
+                           prior_used_len=prior_used_len, cp_offset=cp_offset,
+                           sliding_window=120)
+
+
+def test_compiled_flash_attention_with_prefix_equals_eager(gpu):
+    a = _fa_inputs(gpu)
+    ref = _fa(**a)
+    out = _compiled(_fa)(**a)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+
+
+def _swa(B, prior, fp8, dev, seed):
+    from test_gpu_swa_fused import _layer
+    a = _layer(B, 128, 256, 8, 2, 64, 64, prior, 64, fp8, seed)
+    return {k: (v.to(dev) if torch.is_tensor(v) else v) for k, v in a.items()}
+
+
+def _swa_call(a):
+    return swa_fused_attention(**a)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_compiled_swa_fused_equals_eager(gpu, fp8):
+    a = _swa(2, 90, fp8, gpu, seed=31)
+    a2 = {k: (v.clone() if torch.is_tensor(v) else v) for k, v in a.items()}
+    out_r, kc_r, vc_r = _swa_call(a)
+    out, kc, vc = _compiled(_swa_call)(a2)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out_r)
+    # the in-place cache write happened under compile, to the same bytes
+    assert torch.equal(a2["k_cache"].view(torch.uint8), kc_r.view(torch.uint8))
+    assert torch.equal(a2["v_cache"].view(torch.uint8), vc_r.view(torch.uint8))
+
+
+def _qkv_args(dev):
+    from oracle import swa_fused as OS
+    from test_gpu_qkv import _qkv_inputs
+    B, S, H, Hq, Hkv, d, bs, nb = 2, 24, 512, 8, 2, 128, 16, 12
+    t = _qkv_inputs(B, S, H, Hq, Hkv, d, seed=70)
+    cos, sin = OS.make_rope(B, S, d, 40)
+    g = torch.Generator().manual_seed(71)
+    slots = torch.randperm(nb * bs, generator=g)[:B * S].reshape(B, S)
+    kc = torch.randn(nb, Hkv, bs, d, generator=g).to(torch.bfloat16)
+    return dict(x=t["x"].to(dev), w=t["w"].to(dev), b=t["b"].to(dev), cos=cos.to(dev),
+                sin=sin.to(dev), kc=kc.to(dev), vc=kc.clone().to(dev), slots=slots.to(dev),
+                d=d, Hq=Hq, Hkv=Hkv, bs=bs)
+
+
+def _qkv_call(x, w, b, cos, sin, kc, vc, slots, d, Hq, Hkv, bs):
+    q, _, _ = qkv_proj(x, w, bias=b, d_head=d, cos_cache=cos, sin_cache=sin, num_q_heads=Hq,
+                       num_kv_heads=Hkv, k_cache=kc, v_cache=vc, use_block_kv=True,
+                       block_size=bs, slot_mapping=slots)
+    return q
+
+
+def test_compiled_qkv_proj_with_cache_write_equals_eager(gpu):
+    a = _qkv_args(gpu)
+    a2 = {k: (v.clone() if torch.is_tensor(v) else v) for k, v in a.items()}
+    ref = _qkv_call(**a)
+    out = _compiled(_qkv_call)(**a2)
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    assert torch.equal(a2["kc"], a["kc"]) and torch.equal(a2["vc"], a["vc"])
+
+
+def _capture(fn):
+    """Warm up on a side stream, then capture one call of ``fn``."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        res = fn()
+    return graph, res
+
+
+def test_hip_graph_flash_attention_reads_prior_len_at_replay(gpu):
+    a = _fa_inputs(gpu)
+    graph, out = _capture(lambda: _fa(**a))
+    for used, cp in ((97, 5), (150, 0), (0, 3), (33, 40)):
+        a["prior_used_len"].fill_(used)
+        a["cp_offset"].fill_(cp)
+        ref = _fa(**a)            # eager with the same device values
+        out.zero_()
+        noise = torch.randn(1 << 20, device=gpu).sum()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(noise)
+        assert torch.equal(out, ref), f"prior_used_len {used}, cp_offset {cp}"
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_hip_graph_swa_fused_reads_prior_at_replay(gpu, fp8):
+    a = _swa(2, 90, fp8, gpu, seed=32)
+    kc0, vc0 = a["k_cache"].clone(), a["v_cache"].clone()
+    graph, (out, _, _) = _capture(lambda: _swa_call(a))
+    for prior in (90, 0, 64, 127):
+        a["prior_tokens"].fill_(prior)
+        a["k_cache"].copy_(kc0)
+        a["v_cache"].copy_(vc0)
+        ref, kc_r, vc_r = _swa_call(a)
+        ref, kc_r, vc_r = ref.clone(), kc_r.clone(), vc_r.clone()
+        a["k_cache"].copy_(kc0)
+        a["v_cache"].copy_(vc0)
+        out.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref), f"prior {prior}"
+        assert torch.equal(a["k_cache"].view(torch.uint8), kc_r.view(torch.uint8))
+        assert torch.equal(a["v_cache"].view(torch.uint8), vc_r.view(torch.uint8))
+
+
+def test_hip_graph_segmented_and_qkv_proj_replay_equal_eager(gpu):
+    cfg = W.PrefillConfig("t", 1, 16, 2, 128, 32, 200, 300, 300, seed=19)
+    pb = W.make_prefill_batch(cfg, gpu)
+    ops.kv_write(pb.k_new, pb.v_new, pb.slots, pb.k_cache, pb.v_cache)
+    q = pb.q.transpose(0, 1).contiguous()
+    prior = pb.prior.view(1, 1).clone()
+    qa = _qkv_args(gpu)
+    kc0 = qa["kc"].clone()
+
+    def work():
+        o = segmented_attention(q, pb.k_cache, pb.v_cache, pb.block_table, prior,
+                                cfg.block_size, 0, sliding_window=96)
+        return o, _qkv_call(**qa)
+
+    graph, (out_s, out_q) = _capture(work)
+    for p in (300, 250, 17):
+        prior.fill_(p)
+        qa["kc"].copy_(kc0)
+        qa["vc"].copy_(kc0)
+        ref_s, ref_q = (t.clone() for t in work())
+        kc_ref = qa["kc"].clone()
+        qa["kc"].copy_(kc0)
+        qa["vc"].copy_(kc0)
+        out_s.zero_()
+        out_q.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_s, ref_s), f"segmented, prior {p}"
+        assert torch.equal(out_q, ref_q) and torch.equal(qa["kc"], kc_ref)

@@ -401,17 +401,20 @@ def test_one_pass_full_mask_mode(gpu):
 
 def test_decode_rejects_table_offsets_past_2_31(gpu):
     """The split kernel forms block-table offsets in 32 bits: a table whose
-    last row starts 2^31 entries after its first is rejected before any
-    launch.  The table is a real view of a 16 GiB allocation, so even a
-    launch would read only allocated memory."""
+    last entry lies 2^31 entries or more after its first is rejected before
+    any launch.  The table is a strided view of one 8 GiB allocation (its
+    rows 2^31 / (B - 1) entries apart), so even a launch would read only
+    allocated memory."""
     cfg = _small_cfg(**CASES[1])
     b = _make(cfg, gpu)
     B, nblk = b.block_table.shape[0], b.block_table.shape[-1]
     assert B >= 2 and b.block_table.dim() == 2
-    wide = torch.empty((B, (1 << 31) + 64), dtype=b.block_table.dtype, device=gpu)
-    wide[:, :nblk] = b.block_table
-    b.block_table = wide[:, :nblk]
+    stride = -(-((1 << 31) - (nblk - 1)) // (B - 1))   # (B-1)*stride + nblk - 1 >= 2^31
+    flat = torch.empty((B - 1) * stride + nblk, dtype=b.block_table.dtype, device=gpu)
+    wide = flat.as_strided((B, nblk), (stride, 1))
+    wide.copy_(b.block_table)
+    b.block_table = wide
     with pytest.raises(ValueError, match="2\\^31"):
         _run_core(b)
-    del wide
+    del wide, flat
     torch.cuda.empty_cache()

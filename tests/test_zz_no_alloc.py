@@ -62,3 +62,20 @@ def test_noalloc_decode_rejects_oversized_plans():
         K.paged_decode(q, kn, kn, cache, cache, table, softmax_scale=d ** -0.5, pos_ids=pos,
                        no_alloc=True)
     assert N.DECODE_NOALLOC_SCRATCH_BYTES == 64 << 20
+
+
+def test_noalloc_one_pass_shape_with_a_large_split_layout():
+    """A short-table call (one-pass kernel, partials in LDS) whose split-K
+    layout would exceed the static scratch (1024 rows, 128 q / 8 kv heads:
+    16 query columns, ~600 MB) runs allocation-free and equals the workspace
+    path; then a smaller batch of the same shape family."""
+    dev = torch.device("cuda:0")
+    for B, seed in ((1024, 81), (37, 82)):
+        cfg = W.DecodeConfig(f"onepass_b{B}", B, 128, 8, 128, 32, 60, 250, sink=True, seed=seed)
+        print(f"no-alloc one-pass decode: B={B}", flush=True)
+        b = W.make_decode_batch(cfg, dev)
+        ref = _decode(b, cfg, no_alloc=False)
+        got = _decode(b, cfg, no_alloc=True)
+        torch.cuda.synchronize()
+        assert torch.isfinite(got.float()).all()
+        assert torch.equal(got, ref), f"B={B}: no-alloc output differs"

@@ -275,7 +275,9 @@ __global__ __launch_bounds__(256) void stage_rows_kernel(mia_stage_args a) {
   __shared__ uint16_t tile[kStageRows * kStagePitch];
   const int64_t h = blockIdx.y;
   const int t0 = blockIdx.x * kStageRows;
-  const int D = a.head_dim, Dp = a.out_dim, P = a.prior_rows, S = a.rows;
+  const int D = a.head_dim, Dp = a.out_dim, S = a.rows;
+  // prior rows: the host count, or the device count clamped to the capacity
+  const int P = a.prior_rows_dev ? min(max(*a.prior_rows_dev, 0), a.prior_rows) : a.prior_rows;
   const bool row_fast = a.src_stride[1] == 1 && a.src_stride[2] != 1;  // d-major source
   auto region = [&](const void *p, const int64_t *st, bool vec_extra) {
     StageRegion g;

@@ -1311,6 +1311,9 @@ DecodePlan plan_decode(const mia_decode_args &a) {
   ml_bytes = (ml_bytes + 255) & ~(size_t)255;
   pl.ws_bytes = o_bytes + ml_bytes + ((size_t)a.batch + 2) * sizeof(int32_t) +
                 (size_t)a.batch * a.num_kv_heads * sizeof(int32_t);
+  // the one-pass kernel keeps its partials in LDS and reads no workspace:
+  // a token size (never 0, which callers read as a failed query)
+  if (pl.one_pass) pl.ws_bytes = 256;
   return pl;
 }
 

@@ -675,11 +675,14 @@ def scatter_rows(rows: torch.Tensor, cache: torch.Tensor, block_idx: torch.Tenso
 
 
 def stage_rows(rows: torch.Tensor, prior: Optional[torch.Tensor], prior_rows: int,
-               out_rows: int, out_dim: int) -> torch.Tensor:
-    """``[H, out_rows, out_dim]`` bf16: the first ``prior_rows`` rows of
-    ``prior`` then ``rows`` (both ``[H, *, D]`` views with any strides),
-    zeros in the tail rows and the padded head dims (the prefix
-    concatenation and layout transposes of the dense attention inputs)."""
+               out_rows: int, out_dim: int,
+               prior_rows_dev: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``[H, out_rows, out_dim]`` bf16: the first ``P`` rows of ``prior``
+    then ``rows`` (both ``[H, *, D]`` views with any strides), zeros in the
+    tail rows and the padded head dims (the prefix concatenation and layout
+    transposes of the dense attention inputs).  ``P`` is ``prior_rows``, or,
+    with ``prior_rows_dev`` (device int32 ``[1]``), that count clamped to
+    ``[0, prior_rows]`` read by the kernel (no host read of it)."""
     dev = N.require_gpu(rows) if prior is None else N.require_gpu(rows, prior)
     if rows.dtype != torch.bfloat16 or (prior is not None and prior.dtype != torch.bfloat16):
         raise NotImplementedError("stage_rows: bf16 only")
@@ -687,6 +690,10 @@ def stage_rows(rows: torch.Tensor, prior: Optional[torch.Tensor], prior_rows: in
     if prior_rows and (prior is None or prior.shape[0] != H or prior.shape[1] < prior_rows
                        or prior.shape[2] != D):
         raise ValueError("prior must be [H, >= prior_rows, D]")
+    if prior_rows_dev is not None:
+        N.require_gpu(prior_rows_dev)
+        if prior_rows_dev.dtype != torch.int32 or prior_rows_dev.numel() < 1:
+            raise ValueError("prior_rows_dev must be a device int32 tensor of at least 1 entry")
     out = torch.empty((H, out_rows, out_dim), dtype=torch.bfloat16, device=dev)
     a = N.StageArgs()
     a.src = rows.data_ptr()
@@ -698,6 +705,8 @@ def stage_rows(rows: torch.Tensor, prior: Optional[torch.Tensor], prior_rows: in
     a.dst_stride = _arr(ctypes.c_int64, [out.stride(0), out.stride(1)])
     a.num_heads, a.rows, a.prior_rows = H, S, int(prior_rows)
     a.out_rows, a.head_dim, a.out_dim = int(out_rows), D, int(out_dim)
+    if prior_rows_dev is not None:
+        a.prior_rows_dev = prior_rows_dev.data_ptr()
     N.check(N.lib().mia_stage_rows(ctypes.byref(a), N.stream_ptr(dev)), "stage_rows")
     return out
 

@@ -162,6 +162,7 @@ class StageArgs(ctypes.Structure):
         ("src", c_vp), ("src_stride", c_i64 * 3), ("prior", c_vp), ("prior_stride", c_i64 * 3),
         ("dst", c_vp), ("dst_stride", c_i64 * 2), ("num_heads", c_i32), ("rows", c_i32),
         ("prior_rows", c_i32), ("out_rows", c_i32), ("head_dim", c_i32), ("out_dim", c_i32),
+        ("prior_rows_dev", c_vp),
     ]
 
 

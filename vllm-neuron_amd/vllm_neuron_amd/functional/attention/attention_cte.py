@@ -35,6 +35,7 @@ import torch
 from torch import Tensor
 
 from ... import ops as K
+from . import _meta as M
 
 _TILE = 64  # keys per kernel tile (the padded key buffer is a whole number of tiles)
 
@@ -46,38 +47,32 @@ def _key_rows(x: Tensor, tokens_last: bool) -> Tensor:
 
 def _kernel_rows_ok(x: Tensor, Dp: int) -> bool:
     """Can the kernels read ``x [H, S, D]`` in place: d == Dp contiguous,
-    16-byte aligned rows and base."""
+    16-byte aligned rows and base.  Under torch.compile the address is not
+    known while tracing, so the compiled graph always stages (a copy: the
+    results are the same bits)."""
+    if torch.compiler.is_compiling():
+        return False
     return (x.shape[-1] == Dp and x.stride(-1) == 1 and x.data_ptr() % 16 == 0
             and (x.stride(0) * 2) % 16 == 0 and (x.stride(1) * 2) % 16 == 0)
 
 
-def _paged_view(rows: Tensor, prior: Optional[Tensor], P: int, Lp: int, Dp: int) -> Tensor:
+def _paged_view(rows: Tensor, prior: Optional[Tensor], P: int, Lp: int, Dp: int,
+                P_dev: Optional[Tensor] = None) -> Tensor:
     """Keys or values ``[H, S, D]`` (token-major view) as a paged cache
     ``[Lp/64, H, 64, Dp]`` read through an identity block table.  Used in
     place when it already is one (no prior rows, d == Dp, whole tiles,
-    aligned), otherwise staged once."""
+    aligned), otherwise staged once; with ``P_dev`` the staging kernel reads
+    the prior row count (at most ``P``) from device memory."""
     H, S, D = rows.shape
     if P or S != Lp or not _kernel_rows_ok(rows, Dp):
-        rows = K.stage_rows(rows, prior, P, Lp, Dp)
+        rows = K.stage_rows(rows, prior, P, Lp, Dp, prior_rows_dev=P_dev)
     st, sh = rows.stride(1), rows.stride(0)
     return torch.as_strided(rows, (Lp // _TILE, H, _TILE, Dp), (_TILE * st, sh, st, 1))
 
 
-_META: dict = {}
-
-
-def _metadata(dev, S_q: int, P: int, L: int, nblk: int):
-    """Device copies of cu_seqlens [0, S_q], prior [P], kv_len [L] and the
-    identity block table, made once per shape (read-only)."""
-    key = (str(dev), S_q, P, L, nblk)
-    m = _META.get(key)
-    if m is None:
-        d = torch.tensor([0, S_q, P, L], dtype=torch.int32).to(dev)
-        m = (d[0:2], d[2:3], d[3:4], torch.arange(nblk, dtype=torch.int32, device=dev).view(1, nblk))
-        if len(_META) >= 64:
-            _META.clear()
-        _META[key] = m
-    return m
+def _device_i32(x: Tensor, dev) -> Tensor:
+    """First element of ``x`` as a device int32 ``[1]`` (no host read)."""
+    return x.reshape(-1)[:1].to(device=dev, dtype=torch.int32)
 
 
 def flash_attention(
@@ -129,18 +124,40 @@ def flash_attention(
     kr = _key_rows(k, not tp_k)                       # [B_kv, S_k, D]
     if tuple(kr.shape) != (B_kv, S_k, D):
         raise ValueError(f"k shape {tuple(k.shape)} does not match v {tuple(v.shape)}")
-    P = 0
+    # Prefix rows: the staged key buffer holds all rows of k_prior / v_prior
+    # the caller passed (a static count), and the kernels read how many of
+    # them are used (prior_used_len) and the query offset (cp_offset) from
+    # device memory, so the call never reads a device value on the host
+    # (graph capture, torch.compile).  prior_used_len is clamped to
+    # [0, rows of k_prior] as the reference's slice k_prior[:, :len] is.
+    P_cap = 0
+    P_dev = None
+    kp = None
     if k_prior is not None:
-        P = int(prior_used_len.reshape(-1)[0].item())
-        if P < 0:
-            raise ValueError("prior_used_len must be non-negative")
+        kp = _key_rows(k_prior, not tp_k)             # [B_kv, S_prior, D]
+        if kp.shape[0] != B_kv or kp.shape[2] != D or v_prior.shape[0] != B_kv \
+                or v_prior.shape[2] != D:
+            raise ValueError(f"k_prior {tuple(k_prior.shape)} / v_prior "
+                             f"{tuple(v_prior.shape)} do not match k and v")
+        if kp.dtype != torch.bfloat16 or v_prior.dtype != torch.bfloat16:
+            raise NotImplementedError("flash_attention: bf16 tensors only")
+        P_cap = min(kp.shape[1], v_prior.shape[1])
+        P_dev = _device_i32(prior_used_len, dev).clamp(0, P_cap)
     Dp = 64 if D <= 64 else 128
-    L = P + S_k
-    Lp = max(_TILE, (L + _TILE - 1) // _TILE * _TILE)
+    L_cap = P_cap + S_k
+    Lp = max(_TILE, (L_cap + _TILE - 1) // _TILE * _TILE)
     nblk = Lp // _TILE
-    k_cache = _paged_view(kr, _key_rows(k_prior, not tp_k) if P else None, P, Lp, Dp)
-    v_cache = _paged_view(v, v_prior if P else None, P, Lp, Dp)
-    cu, prior, kv_len, table = _metadata(dev, S_q, P, L, nblk)
+    k_cache = _paged_view(kr, kp, P_cap, Lp, Dp, P_dev)
+    v_cache = _paged_view(v, v_prior if P_cap else None, P_cap, Lp, Dp, P_dev)
+    cu = M.device_i32(dev, (0, S_q))
+    table = M.identity_table(dev, nblk)
+    # keys [0, P + S_k) exist; query i sits at position i + P + cp_offset
+    if P_dev is None:
+        kv_len = M.device_i32(dev, (S_k,))
+        qpos0 = _device_i32(cp_offset, dev) if cp_offset is not None else M.device_i32(dev, (0,))
+    else:
+        kv_len = P_dev + S_k
+        qpos0 = P_dev + _device_i32(cp_offset, dev) if cp_offset is not None else P_dev
 
     # queries [T = S_q, Hq = B, Dp] and the output through strided views
     qp = qr if _kernel_rows_ok(qr, Dp) else K.stage_rows(qr, None, 0, S_q, Dp)
@@ -148,16 +165,15 @@ def flash_attention(
     q_view = qp.permute(1, 0, 2)
     out_view = out.permute(1, 0, 2)
 
-    q_off = int(cp_offset.reshape(-1)[0].item()) if cp_offset is not None else 0
     bmin = bmax = None
     if bound_min is not None:
         # [B, S_q, 1] -> [T = S_q, Hq = B]
         bmin = bound_min.reshape(B, S_q).to(torch.int32).transpose(0, 1)
         bmax = bound_max.reshape(B, S_q).to(torch.int32).transpose(0, 1)
     sk = None if sink is None else sink.reshape(B).float()
-    K.paged_prefill(q_view, cu, prior, S_q, k_cache, v_cache, table, scale=float(scale),
+    K.paged_prefill(q_view, cu, qpos0, S_q, k_cache, v_cache, table, scale=float(scale),
                     sliding_window=sliding_window if causal_mask else 0, sink=sk,
-                    out=out_view, kv_len=kv_len, non_causal=not causal_mask, q_offset=q_off,
+                    out=out_view, kv_len=kv_len, non_causal=not causal_mask, q_offset=0,
                     bound_min=bmin, bound_max=bmax, empty_rows_uniform=True)
     res = out if Dp == D else out[:, :, :D]
     return res.transpose(-2, -1) if tp_out else res

@@ -230,6 +230,11 @@ def attention_decode(
         raise NotImplementedError("attention_decode does not support is_h_transposed_by_4=True")
     if K_cache_transposed:
         raise NotImplementedError("attention_decode reads the standard K cache layout only")
+    if transposed_out:
+        # the reference's torch path never reads the flag and its kernel-side
+        # layout is defined inside the absent NKI library: refuse it rather
+        # than return the untransposed layout
+        raise NotImplementedError("attention_decode does not support transposed_out=True")
     if attention_dp > 1 or kv_needs_a2a or dcp_size > 1:
         raise NotImplementedError(
             "attention DP / DCP span several devices; this library runs on one GPU")

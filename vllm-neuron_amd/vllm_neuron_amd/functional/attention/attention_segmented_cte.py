@@ -26,6 +26,7 @@ import torch
 from torch import Tensor
 
 from ... import ops as K
+from . import _meta as M
 from .attention_decode import _unswizzle_packed_k
 
 _MAX_HEAD_DIM = 128
@@ -89,7 +90,7 @@ def segmented_attention(
     dev = q.device
     if q.stride(2) != 1 or (q.stride(0) * 2) % 16 or (q.stride(1) * 2) % 16:
         q = q.contiguous()
-    cu = torch.tensor([0, S_q], dtype=torch.int32, device=dev)
+    cu = M.device_i32(dev, (0, S_q))   # made once per (device, S_q): no copy per call
     prior = prior_tokens.reshape(-1)[:1]
     table = block_tables[:1]
     out = torch.empty((Nh, S_q, D), dtype=torch.bfloat16, device=dev)

@@ -39,19 +39,30 @@ from ... import _native as N
 from .attention_cte import flash_attention
 
 
-def _prior_window(k_cache: Tensor, v_cache: Tensor, table_row: Tensor, start: int, end: int,
-                  fp8_packed: bool, k_s: float, v_s: float) -> Tuple[Tensor, Tensor]:
-    """K/V of prior tokens [start, end) of one sequence as bf16 ``[n, Hkv, d]``
-    (dequantized for an FP8 cache; swa_fused.py:160-177)."""
+def _prior_window(k_cache: Tensor, v_cache: Tensor, block_tables: Tensor, prior: Tensor,
+                  n: int, fp8_packed: bool, k_s: Optional[Tensor],
+                  v_s: Optional[Tensor]) -> Tuple[Tensor, Tensor, Tensor]:
+    """The last ``P = min(prior, n)`` prior tokens of every row as bf16
+    ``[B, n, Hkv, d]`` K and V (rows ``[0, P)`` hold positions ``prior - P ..
+    prior - 1``; the rest are don't-care rows of valid blocks), dequantized
+    for an FP8 cache (swa_fused.py:160-177), and ``P`` as a device int32
+    ``[1]``.  Everything stays on the device: ``prior`` is never read on the
+    host."""
     bs = v_cache.shape[2]
-    idx = torch.arange(start, end, device=table_row.device)
-    blk = table_row[idx // bs].long()
-    off = idx % bs
+    nblk = block_tables.shape[1]
+    P = prior.clamp(max=n)                                    # [1] int64
+    pos = (prior - P + torch.arange(n, device=prior.device)).clamp(0, nblk * bs - 1)
+    blk = block_tables[:, pos // bs].long()                   # [B, n]
+    off = pos % bs                                            # [n]
     if fp8_packed:
         kq = k_cache.view(torch.uint8)[blk, :, off // 2, :, off % 2].view(k_cache.dtype)
         vq = v_cache.view(torch.uint8)[blk, :, off, :].view(v_cache.dtype)
-        return ((kq.float() * k_s).to(torch.bfloat16), (vq.float() * v_s).to(torch.bfloat16))
-    return k_cache[blk, :, off, :].to(torch.bfloat16), v_cache[blk, :, off, :].to(torch.bfloat16)
+        k = (kq.float() * k_s).to(torch.bfloat16)
+        v = (vq.float() * v_s).to(torch.bfloat16)
+    else:
+        k = k_cache[blk, :, off, :].to(torch.bfloat16)
+        v = v_cache[blk, :, off, :].to(torch.bfloat16)
+    return k, v, P.to(torch.int32)
 
 
 def swa_fused_attention(
@@ -97,17 +108,19 @@ def swa_fused_attention(
     N.require_gpu(hidden_states, k_cache, v_cache, block_tables)
     q_dim, kv_dim = num_q_heads * d_head, num_kv_heads * d_head
     bf = torch.bfloat16
-    k_s = float(k_scale.reshape(-1)[0].item()) if k_scale is not None else 1.0
-    v_s = float(v_scale.reshape(-1)[0].item()) if v_scale is not None else 1.0
-    prior_len = int(prior_tokens.reshape(-1)[0].item())
-    n_prior_blocks = (prior_len + block_size - 1) // block_size
+    # device scalars (never read on the host: graph capture, torch.compile)
+    k_s = k_scale.reshape(-1)[:1].to(device=dev, dtype=torch.float32) if k_scale is not None else None
+    v_s = v_scale.reshape(-1)[:1].to(device=dev, dtype=torch.float32) if v_scale is not None else None
+    prior = prior_tokens.reshape(-1)[:1].to(device=dev, dtype=torch.int64)
+    n_prior_blocks = (prior + block_size - 1) // block_size   # [1]
 
     T = B * S
     # only the last sliding_window - 1 prior tokens can be seen by a query;
     # they are read before the active rows are written
-    p0 = max(0, prior_len - (sliding_window - 1))
-    priors = [_prior_window(k_cache, v_cache, block_tables[b], p0, prior_len, fp8_packed, k_s,
-                            v_s) if prior_len > p0 else (None, None) for b in range(B)]
+    n_win = sliding_window - 1
+    if n_win > 0:
+        kp, vp, P = _prior_window(k_cache, v_cache, block_tables, prior, n_win, fp8_packed,
+                                  k_s, v_s)
 
     # 1. projection (library GEMM)
     qkv = torch.addmm(qkv_bias.reshape(1, -1).to(bf), hidden_states.reshape(T, H).to(bf),
@@ -115,15 +128,19 @@ def swa_fused_attention(
     # 2-3. RoPE (fp32), q * scale, split, and the active K/V into the cache at
     # token s -> logical block ceil(prior / bs) + s // bs (prior blocks untouched)
     s_idx = torch.arange(S, device=dev)
-    slots = (block_tables[:, n_prior_blocks + s_idx // block_size].long() * block_size
-             + s_idx % block_size)
+    lblk = n_prior_blocks + s_idx // block_size               # [S] logical blocks
+    nblk = block_tables.shape[1]
+    # a logical block past the table (an index error in the reference) gets
+    # the skipped sentinel slot -1 instead of a host-side check
+    phys = block_tables[:, lblk.clamp(max=nblk - 1)].long()
+    slots = torch.where(lblk < nblk, phys * block_size + s_idx % block_size,
+                        torch.full_like(phys, -1))
     q = torch.empty((B, S, num_q_heads, d_head), dtype=bf, device=dev)
     k = torch.empty((B, S, num_kv_heads, d_head), dtype=bf, device=dev)
     v = torch.empty_like(k)
     ep = dict(slots=slots.reshape(T), k_cache=k_cache, v_cache=v_cache, k_packed=fp8_packed)
     if fp8_packed:
-        ep.update(quant_mode=N.QUANT_DIV_F32, k_scale=k_scale.reshape(-1)[:1],
-                  v_scale=v_scale.reshape(-1)[:1])
+        ep.update(quant_mode=N.QUANT_DIV_F32, k_scale=k_s, v_scale=v_s)
     K.qkv_epilogue(qkv, num_q_heads, num_kv_heads, d_head, rope_mode=K.ROPE_HALF,
                    cos=cos_cache.float().reshape(T, d_head),
                    sin=sin_cache.float().reshape(T, d_head), cos_hi_off=d_head // 2,
@@ -134,11 +151,10 @@ def swa_fused_attention(
     # 4. sliding-window attention, sink in the denominator
     attn = torch.empty((B, S, num_q_heads, d_head), dtype=bf, device=dev)
     for b in range(B):
-        kp, vp = priors[b]
         kw = {}
-        if kp is not None:
-            kw = dict(k_prior=kp.transpose(0, 1), v_prior=vp.transpose(0, 1),
-                      prior_used_len=torch.tensor([prior_len - p0], device=dev))
+        if n_win > 0:
+            kw = dict(k_prior=kp[b].transpose(0, 1), v_prior=vp[b].transpose(0, 1),
+                      prior_used_len=P)
         o = flash_attention(q[b].transpose(0, 1), k[b].transpose(0, 1), v[b].transpose(0, 1),
                             scale=1.0, causal_mask=True, sliding_window=sliding_window,
                             sink=sink[b].reshape(num_q_heads, 1).float(), tp_k=True, **kw)

@@ -116,18 +116,19 @@ def scatter_rows(rows, cache, block_idx, head_idx, pos_idx, *, k_packed=False) -
 
 
 @custom_op("mia::stage_rows", mutates_args=())
-def _stage_rows(rows: Tensor, prior: Optional[Tensor], prior_rows: int, out_rows: int,
-                out_dim: int) -> Tensor:
-    return K.stage_rows(rows, prior, prior_rows, out_rows, out_dim)
+def _stage_rows(rows: Tensor, prior: Optional[Tensor], prior_rows_dev: Optional[Tensor],
+                prior_rows: int, out_rows: int, out_dim: int) -> Tensor:
+    return K.stage_rows(rows, prior, prior_rows, out_rows, out_dim, prior_rows_dev)
 
 
 @_stage_rows.register_fake
-def _(rows, prior, prior_rows, out_rows, out_dim):
+def _(rows, prior, prior_rows_dev, prior_rows, out_rows, out_dim):
     return rows.new_empty((rows.shape[0], out_rows, out_dim), dtype=torch.bfloat16)
 
 
-def stage_rows(rows, prior, prior_rows: int, out_rows: int, out_dim: int) -> Tensor:
-    return _stage_rows(rows, prior, int(prior_rows), int(out_rows), int(out_dim))
+def stage_rows(rows, prior, prior_rows: int, out_rows: int, out_dim: int,
+               prior_rows_dev=None) -> Tensor:
+    return _stage_rows(rows, prior, prior_rows_dev, int(prior_rows), int(out_rows), int(out_dim))
 
 
 # ---------------------------------------------------------------------------
@@ -208,17 +209,10 @@ def swa_trim(block_table, ctx_lens, num_swa_blocks: int, block_size: int):
 # ---------------------------------------------------------------------------
 # attention: paged decode and paged (varlen) prefill
 # ---------------------------------------------------------------------------
-@custom_op("mia::paged_decode", mutates_args=("k_cache", "v_cache", "out", "workspace"))
-def _paged_decode(q: Tensor, k_new: Tensor, v_new: Tensor, k_cache: Tensor, v_cache: Tensor,
-                  block_table: Tensor, out: Tensor, workspace: Optional[Tensor],
-                  pos_ids: Optional[Tensor], start_pos: Optional[Tensor],
-                  active_mask: Optional[Tensor], full_mask: Optional[Tensor],
-                  sink: Optional[Tensor], k_dequant: Optional[Tensor],
-                  v_dequant: Optional[Tensor], k_quant: Optional[Tensor],
-                  v_quant: Optional[Tensor], write_slots: Optional[Tensor],
-                  softmax_scale: float, mask_block_len: int, quant_mode: int,
-                  quant_per_head: bool, split_tokens: int, k_packed: bool,
-                  no_alloc: bool) -> None:
+def _decode_launch(q, k_new, v_new, k_cache, v_cache, block_table, out, workspace, pos_ids,
+                   start_pos, active_mask, full_mask, sink, k_dequant, v_dequant, k_quant,
+                   v_quant, write_slots, softmax_scale, mask_block_len, quant_mode,
+                   quant_per_head, split_tokens, k_packed, no_alloc) -> None:
     K.paged_decode(q, k_new, v_new, k_cache, v_cache, block_table, softmax_scale=softmax_scale,
                    pos_ids=pos_ids, start_pos=start_pos, active_mask=active_mask,
                    full_mask=full_mask, mask_block_len=mask_block_len, sink=sink,
@@ -228,7 +222,50 @@ def _paged_decode(q: Tensor, k_new: Tensor, v_new: Tensor, k_cache: Tensor, v_ca
                    k_packed=k_packed, no_alloc=no_alloc)
 
 
+# Two ops for one kernel pair: the attention alone reads the caches
+# (functionalization then never copies them), the variant with the fused
+# cache write (stage 8) declares both caches written.
+@custom_op("mia::paged_decode", mutates_args=("out", "workspace"))
+def _paged_decode(q: Tensor, k_new: Tensor, v_new: Tensor, k_cache: Tensor, v_cache: Tensor,
+                  block_table: Tensor, out: Tensor, workspace: Optional[Tensor],
+                  pos_ids: Optional[Tensor], start_pos: Optional[Tensor],
+                  active_mask: Optional[Tensor], full_mask: Optional[Tensor],
+                  sink: Optional[Tensor], k_dequant: Optional[Tensor],
+                  v_dequant: Optional[Tensor], k_quant: Optional[Tensor],
+                  v_quant: Optional[Tensor], softmax_scale: float, mask_block_len: int,
+                  quant_mode: int, quant_per_head: bool, split_tokens: int, k_packed: bool,
+                  no_alloc: bool) -> None:
+    _decode_launch(q, k_new, v_new, k_cache, v_cache, block_table, out, workspace, pos_ids,
+                   start_pos, active_mask, full_mask, sink, k_dequant, v_dequant, k_quant,
+                   v_quant, None, softmax_scale, mask_block_len, quant_mode, quant_per_head,
+                   split_tokens, k_packed, no_alloc)
+
+
 @_paged_decode.register_fake
+def _(q, k_new, v_new, k_cache, v_cache, block_table, out, workspace, pos_ids, start_pos,
+      active_mask, full_mask, sink, k_dequant, v_dequant, k_quant, v_quant, softmax_scale,
+      mask_block_len, quant_mode, quant_per_head, split_tokens, k_packed, no_alloc):
+    return None
+
+
+@custom_op("mia::paged_decode_write", mutates_args=("k_cache", "v_cache", "out", "workspace"))
+def _paged_decode_write(q: Tensor, k_new: Tensor, v_new: Tensor, k_cache: Tensor,
+                        v_cache: Tensor, block_table: Tensor, out: Tensor,
+                        workspace: Optional[Tensor], pos_ids: Optional[Tensor],
+                        start_pos: Optional[Tensor], active_mask: Optional[Tensor],
+                        full_mask: Optional[Tensor], sink: Optional[Tensor],
+                        k_dequant: Optional[Tensor], v_dequant: Optional[Tensor],
+                        k_quant: Optional[Tensor], v_quant: Optional[Tensor],
+                        write_slots: Tensor, softmax_scale: float, mask_block_len: int,
+                        quant_mode: int, quant_per_head: bool, split_tokens: int,
+                        k_packed: bool, no_alloc: bool) -> None:
+    _decode_launch(q, k_new, v_new, k_cache, v_cache, block_table, out, workspace, pos_ids,
+                   start_pos, active_mask, full_mask, sink, k_dequant, v_dequant, k_quant,
+                   v_quant, write_slots, softmax_scale, mask_block_len, quant_mode,
+                   quant_per_head, split_tokens, k_packed, no_alloc)
+
+
+@_paged_decode_write.register_fake
 def _(q, k_new, v_new, k_cache, v_cache, block_table, out, workspace, pos_ids, start_pos,
       active_mask, full_mask, sink, k_dequant, v_dequant, k_quant, v_quant, write_slots,
       softmax_scale, mask_block_len, quant_mode, quant_per_head, split_tokens, k_packed,
@@ -243,7 +280,8 @@ def paged_decode(q, k_new, v_new, k_cache, v_cache, block_table, *, softmax_scal
                  quant_per_head: bool = False, out=None, workspace=None, split_tokens: int = 0,
                  split_events=None, write_slots=None, k_packed: bool = False,
                  no_alloc: bool = False) -> Tensor:
-    """``_kernels.paged_decode`` through the ``mia::paged_decode`` op;
+    """``_kernels.paged_decode`` through ``mia::paged_decode`` (no cache
+    write) or ``mia::paged_decode_write`` (with ``write_slots``);
     ``split_events`` (timing instrumentation, eager only) calls the kernel
     wrapper directly."""
     if split_events is not None:
@@ -258,10 +296,14 @@ def paged_decode(q, k_new, v_new, k_cache, v_cache, block_table, *, softmax_scal
                               k_packed=k_packed, no_alloc=no_alloc)
     if out is None:
         out = q.new_empty(q.shape, dtype=torch.bfloat16)
-    _paged_decode(q, k_new, v_new, k_cache, v_cache, block_table, out, workspace, pos_ids,
-                  start_pos, active_mask, full_mask, sink, k_dequant, v_dequant, k_quant, v_quant,
-                  write_slots, float(softmax_scale), int(mask_block_len), int(quant_mode),
-                  bool(quant_per_head), int(split_tokens), bool(k_packed), bool(no_alloc))
+    common = (q, k_new, v_new, k_cache, v_cache, block_table, out, workspace, pos_ids, start_pos,
+              active_mask, full_mask, sink, k_dequant, v_dequant, k_quant, v_quant)
+    scal = (float(softmax_scale), int(mask_block_len), int(quant_mode), bool(quant_per_head),
+            int(split_tokens), bool(k_packed), bool(no_alloc))
+    if write_slots is None:
+        _paged_decode(*common, *scal)
+    else:
+        _paged_decode_write(*common, write_slots, *scal)
     return out
 
 
@@ -382,6 +424,7 @@ def row_norm(x, mode: int, eps: float, gamma=None, beta=None, *, add0=None, add1
 
 OPS: List[str] = [
     "kv_write", "gather_kv", "packed_k_convert", "scatter_rows", "stage_rows", "decode_mask",
-    "slot_mapping", "remap_null_block", "swa_trim", "paged_decode", "paged_prefill",
+    "slot_mapping", "remap_null_block", "swa_trim", "paged_decode", "paged_decode_write",
+    "paged_prefill",
     "qkv_epilogue", "row_norm",
 ]
