@@ -6,7 +6,10 @@ head_dim 128, bf16, batch 64, contexts U[512, 8192], block_size 32, random
 non-contiguous block tables, N(0,1) inputs.  A step is one decode attention
 pass over the batch: the split-K attention kernel plus the combine kernel,
 which also writes the 64 new tokens' K/V rows into the cache; inputs are
-resident in HBM.
+resident in HBM.  Every decode call states vLLM's block ownership (each
+row writes its new token into a block no other row reads:
+``write_slots_private``), which lets short tables write the cache inside
+the attention kernel.
 
 The same line carries
   * ``roofline`` for the dominant kernel (the split-K decode kernel, HBM
@@ -60,7 +63,8 @@ def _decode_step_fn(b, dev):
         return paged_decode_core(b.q, b.k_new, b.v_new, b.k_cache, b.v_cache, b.block_table,
                                  block_len=cfg.block_size, S_ctx=S_ctx, pos_ids=b.pos,
                                  softmax_scale=cfg.head_dim ** -0.5, workspace=ws,
-                                 split_events=events, write_slots=slots)
+                                 split_events=events, write_slots=slots,
+                                 write_slots_private=True)
 
     return step
 
@@ -209,7 +213,7 @@ def bench_secondary(dev, reps: int, cpu_rows: int = 0) -> dict:
                               block_len=cfg.block_size, S_ctx=S_ctx, pos_ids=b.pos,
                               swa_start_pos_ids=b.start, sink=b.sink,
                               softmax_scale=cfg.head_dim ** -0.5, workspace=ws,
-                              write_slots=slots, **kw)
+                              write_slots=slots, write_slots_private=True, **kw)
 
         us = _graph_us(step, dev, reps)
         nbytes = W.decode_bytes(b)

@@ -253,7 +253,13 @@ typedef struct {
    * outside [0, num_blocks * block_size) are skipped.  I32 / I64 / U32. */
   const void *write_slots;
   int32_t write_slot_dtype;
-  int32_t _pad2;
+  /* Non-zero: the caller guarantees that no row of the call attends to
+   * another row's write slot (each row writes into blocks only it reads, as
+   * vLLM's block ownership gives), so a row's rows may be written as soon as
+   * that row has read the cache; lets the short-table (one-pass) kernel
+   * write them itself instead of a scatter launch after it.  0 keeps the
+   * reference's order: every write after every read. */
+  int32_t write_private;
 } mia_decode_args;
 
 size_t mia_decode_workspace_bytes(const mia_decode_args *args);

@@ -133,7 +133,7 @@ def test_opcheck_registered_ops(gpu):
               None, None, None, None, None, None, None)
     scal = (0.125, 0, 0, False, 0, False, False)
     torch.library.opcheck(torch.ops.mia.paged_decode.default, (*common, *scal))
-    torch.library.opcheck(torch.ops.mia.paged_decode_write.default, (*common, slots, *scal))
+    torch.library.opcheck(torch.ops.mia.paged_decode_write.default, (*common, slots, *scal, True))
     pcfg = W.PrefillConfig("t", 1, 8, 2, 64, 16, 40, 32, 32, seed=5)
     pb = W.make_prefill_batch(pcfg, gpu)
     pout = torch.empty_like(pb.q)

@@ -418,3 +418,61 @@ def test_decode_rejects_table_offsets_past_2_31(gpu):
         _run_core(b)
     del wide, flat
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("case,ctx_hi,packed", [(0, 200, False), (3, 900, False),
+                                                 (7, 200, False), (7, 200, True),
+                                                 (8, 500, True), (1, 1000, False)])
+def test_private_write_slots_match_the_reference_order(gpu, case, ctx_hi, packed):
+    """``write_slots_private`` (no row attends to another row's write slot):
+    the short-table kernel writes each row's K/V itself, right after its own
+    reads, instead of a scatter launch after the attention.  With each row's
+    slots at its own active positions (vLLM's block ownership) the output
+    equals that kernel's without a write and every cache byte equals the
+    default order's (a scatter after the reads), one and two active
+    tokens, bf16 and FP8 caches (K packed or not), tables of up to 8 and up
+    to 32 tiles."""
+    from vllm_neuron_amd.functional.attention.attention_decode import _swizzle_packed_k
+    cfg = _small_cfg(**dict(CASES[case], ctx_lo=1, ctx_hi=ctx_hi, max_model_len=0))
+    for S in (1, 2):
+        b = _make(cfg, gpu, S=S)
+        extra = {}
+        if packed:
+            b.k_cache = _swizzle_packed_k(b.k_cache)
+            extra = dict(fp8_packed=True)
+        B, bs = cfg.batch, cfg.block_size
+        p = b.pos.long()                                     # [B, S] active positions
+        rows = torch.arange(B, device=gpu).view(B, 1)
+        slots = (b.block_table[rows, p // bs].long() * bs + p % bs).reshape(-1)
+        kc, vc = b.k_cache.clone(), b.v_cache.clone()
+        # the same kernel without a write (tables over 8 tiles take the
+        # split path when a write must wait for every row's reads)
+        ref = _run_core(b, **extra)
+        _run_core(b, write_slots=slots, **extra)
+        kr, vr = b.k_cache.clone(), b.v_cache.clone()
+        b.k_cache.copy_(kc)
+        b.v_cache.copy_(vc)
+        got = _run_core(b, write_slots=slots, write_slots_private=True, **extra)
+        torch.cuda.synchronize()
+        assert torch.equal(got, ref), f"S={S}: output differs"
+        assert torch.equal(b.k_cache.view(torch.uint8), kr.view(torch.uint8)), f"S={S}"
+        assert torch.equal(b.v_cache.view(torch.uint8), vr.view(torch.uint8)), f"S={S}"
+
+
+@pytest.mark.parametrize("case", [0, 3, 8])
+@pytest.mark.parametrize("S", [1, 2])
+def test_one_pass_long_tables(gpu, case, S):
+    """d = 64 tables of 17-32 tiles (up to 1024 tokens) with few segments
+    take the one-pass kernel: against float64
+    math and against the split-K path on the same inputs."""
+    cfg = _small_cfg(**dict(CASES[case], ctx_lo=600, ctx_hi=1000, max_model_len=0))
+    b = _make(cfg, gpu, S=S)
+    S_ctx = b.block_table.shape[-1] * cfg.block_size
+    assert 512 < S_ctx <= 1024 and cfg.head_dim == 64
+    one = _run_core(b).float().cpu()
+    split = _run_core(b, split_tokens=32).float().cpu()
+    ref = _fp32(b, cfg.head_dim ** -0.5)
+    tol = TOL_FP8 if cfg.fp8 else TOL_BF16
+    assert (one.double() - ref).abs().max().item() <= tol
+    assert (split.double() - ref).abs().max().item() <= tol
+    assert (one - split).abs().max().item() <= (3e-2 if cfg.fp8 else 1.6e-2)

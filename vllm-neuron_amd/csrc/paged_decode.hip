@@ -62,6 +62,9 @@ constexpr int kWaves = 4;
 // waves of a one-pass workgroup (one segment), two per SIMD (twelve at d =
 // 64 measured equal or slower: the per-wave chain of round trips, not the
 // tiles per wave, sets a short table's time)
+// waves of a one-pass workgroup (12 or 16 for the 17-32 tiles of the
+// Llama-3.2-1B decode, so that each streams fewer tiles one after another:
+// 13.9 -> 14.7 / 16.2 us, slower)
 constexpr int one_waves(int) { return 8; }
 // occupancy the split kernel is compiled for: 2 workgroups per CU (8 waves,
 // 256 VGPRs each).  With streaming V loads an FP8 cache no longer needs a
@@ -255,7 +258,58 @@ struct CombineParams {
   int k_packed;              // K cache in the packed FP8 layout
   uint8_t *k_cache_w;
   uint8_t *v_cache_w;
+  int onepass_write;         // one-pass kernel: write the active rows itself
 };
+
+// The S active K/V rows of segment (b, h) into the cache at their write
+// slots (quantised for an FP8 cache; sentinel slots skipped): one wave,
+// the d values spread over the lanes.  Used by the one-pass kernel when the
+// caller guarantees that no row of the launch attends to another row's
+// write slot (each row writes into a block only it reads: vLLM's block
+// ownership), so the write need not wait for the other rows' reads.
+template <int D>
+MIA_DEV void write_active_rows(const CombineParams &c, int b, int h, int lane) {
+  const DecodeKParams &p = c.k;
+  constexpr int DPL = D / 64;
+  const int64_t max_slot = (int64_t)p.nb * p.bs;
+  const bool fp8 = c.cache_dtype == MIA_DTYPE_FP8_E4M3FN;
+  const float ks = fp8 && c.k_quant ? c.k_quant[c.quant_per_head ? h : 0] : 1.f;
+  const float vs = fp8 && c.v_quant ? c.v_quant[c.quant_per_head ? h : 0] : 1.f;
+#pragma nounroll
+  for (int k = 0; k < p.S; ++k) {
+    const int64_t si = (int64_t)b * p.S + k;
+    int64_t slot;
+    if (c.wslot_dtype == MIA_DTYPE_I64) slot = ((const int64_t *)c.wslots)[si];
+    else if (c.wslot_dtype == MIA_DTYPE_U32) slot = ((const uint32_t *)c.wslots)[si];
+    else slot = ((const int32_t *)c.wslots)[si];
+    if (slot < 0 || slot >= max_slot) continue;  // sentinel: skipped
+    const int64_t blk = slot / p.bs, off = slot % p.bs;
+    // packed K: element e of token off at ((off & ~1) * kc_t + 2 e + (off & 1))
+    const int kstep = c.k_packed ? 2 : 1;
+    const int64_t kd = blk * p.kc_blk + h * p.kc_h +
+                       (c.k_packed ? (off & ~1) * p.kc_t + (off & 1) : off * p.kc_t);
+    const int64_t vd = blk * p.vc_blk + h * p.vc_h + off * p.vc_t;
+    const int64_t kb = b * c.kn_b + (int64_t)k * c.kn_s + (int64_t)h * c.kn_h;
+    const int64_t vb = b * c.vn_b + (int64_t)k * c.vn_s + (int64_t)h * c.vn_h;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) {
+      const int e = lane + 64 * j;
+      const uint16_t kr = c.k_new[kb + e], vr = c.v_new[vb + e];
+      if (fp8) {
+        const float kx = bf16_bits_to_f32(kr), vx = bf16_bits_to_f32(vr);
+        c.k_cache_w[kd + kstep * e] = (uint8_t)(c.quant_mode == MIA_QUANT_NONE
+                                                    ? f32_to_e4m3fn_bits(kx)
+                                                    : quantize_e4m3fn(kx, ks, c.quant_mode));
+        c.v_cache_w[vd + e] = (uint8_t)(c.quant_mode == MIA_QUANT_NONE
+                                            ? f32_to_e4m3fn_bits(vx)
+                                            : quantize_e4m3fn(vx, vs, c.quant_mode));
+      } else {
+        ((uint16_t *)c.k_cache_w)[kd + e] = kr;
+        ((uint16_t *)c.v_cache_w)[vd + e] = vr;
+      }
+    }
+  }
+}
 
 MIA_DEV float quant_roundtrip(const CombineParams &c, float x, int h, const float *qscale) {
   if (c.quant_mode == MIA_QUANT_NONE) return x;
@@ -347,12 +401,12 @@ MIA_DEV int wave_scan_incl(int x, int lane) {
 
 // PK: the K cache is in the packed FP8 layout (FP8 only).  ONE: one-pass
 // mode (decode_onepass_kernel, P = CombineParams) for short tables:
-// workgroup g takes segment (b, h) = (g / Hkv, g % Hkv), its one_waves(D)
-// waves stream contiguous runs of the segment's tiles, and the
+// workgroup g takes segment (b, h) = (g / Hkv, g % Hkv), its OW waves
+// stream contiguous runs of the segment's tiles, and the
 // first wave merges their (m, l, o) through LDS, adds the active keys and
 // the sink, normalises and stores the bf16 output: no shares, no global
 // partials, no combine launch.
-template <int D, int NCP, bool FP8, bool PK, bool ONE, typename P>
+template <int D, int NCP, bool FP8, bool PK, bool ONE, int OW, typename P>
 MIA_DEV void split_body(const P &c) {
   const DecodeKParams &p = kparams(c);
   static_assert(FP8 || !PK, "packed K is an FP8 layout");
@@ -386,7 +440,7 @@ MIA_DEV void split_body(const P &c) {
   // V tile of each wave, bf16, rows of D elements, 16-byte chunks XOR-
   // swizzled by row (chunk c of token row t at c ^ (t % (D/8))): the writes
   // (16 lanes per row) and the transposed reads below are conflict-free
-  constexpr int NW = ONE ? one_waves(D) : kWaves;  // waves per workgroup
+  constexpr int NW = ONE ? OW : kWaves;  // waves per workgroup
   __shared__ __attribute__((aligned(16))) uint8_t v_lds[NW][kTile * D * 2];
   __shared__ int s_R[kMaxRows + 1];
   __shared__ int s_lo[kMaxRows];
@@ -894,6 +948,29 @@ MIA_DEV void split_body(const P &c) {
         s_one_m[wave][qcol] = m_run;
         s_one_l[wave][qcol] = l_run;
       }
+      // the first active token's K/V rows and the sink, loaded by the
+      // merging wave before the barrier (their latency overlaps the other
+      // waves' runs instead of following the merge)
+      const int hq = cur.h * p.G + g_q;
+      const int64_t kb0 = cur.b * c.kn_b + (int64_t)cur.h * c.kn_h;
+      const int64_t vb0 = cur.b * c.vn_b + (int64_t)cur.h * c.vn_h;
+      uint16_t k0[KSTEPS][8], v0[DB16][4];
+      float sink_v = 0.f;
+      if (wave == 0) {
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) k0[ks][e] = c.k_new[kb0 + kd0(ks, kg) + e];
+#pragma unroll
+        for (int blk = 0; blk < DB16; ++blk)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v0[blk][i] = c.v_new[vb0 + 16 * blk + 4 * kg + i];
+        if (c.sink) sink_v = c.sink[hq];
+      }
+      // private write slots: the row's cache write, by the last wave (its
+      // run is the shortest); no row reads these slots, this one's reads
+      // of them are masked
+      if (c.onepass_write && wave == NW - 1) write_active_rows<D>(c, cur.b, cur.h, lane);
       __syncthreads();
       if (wave != 0) return;
       float m = -INFINITY, l = 0.f;
@@ -916,7 +993,6 @@ MIA_DEV void split_body(const P &c) {
           }
         }
       }
-      const int hq = cur.h * p.G + g_q;
       const float vsc = FP8 ? 256.0f : 1.0f;  // cache V was widened x 2^-8
 #pragma unroll
       for (int blk = 0; blk < DB16; ++blk)
@@ -948,7 +1024,8 @@ MIA_DEV void split_body(const P &c) {
           for (int e = 0; e < 8; ++e) {
             const float qv = __uint_as_float((e & 1) ? (qw[e >> 1] & 0xffff0000u) : (qw[e >> 1] << 16));
             const float kv = quant_roundtrip(
-                c, bf16_bits_to_f32(c.k_new[kb + kd0(ks, kg) + e]), cur.h, c.k_quant);
+                c, bf16_bits_to_f32(k == 0 ? k0[ks][e] : c.k_new[kb + kd0(ks, kg) + e]), cur.h,
+                c.k_quant);
             dot = fmaf(qv, kv, dot);
           }
         }
@@ -968,13 +1045,14 @@ MIA_DEV void split_body(const P &c) {
         for (int blk = 0; blk < DB16; ++blk)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            vv[blk][i] = quant_roundtrip(c, bf16_bits_to_f32(c.v_new[vb + 16 * blk + 4 * kg + i]),
-                                         cur.h, c.v_quant);
+            vv[blk][i] = quant_roundtrip(
+                c, bf16_bits_to_f32(k == 0 ? v0[blk][i] : c.v_new[vb + 16 * blk + 4 * kg + i]),
+                cur.h, c.v_quant);
         absorb(ok ? dot * ascale : -INFINITY, vv, true);
       }
       if (c.sink) {  // the sink logit joins the denominator only
         const float vz[DB16][4] = {};
-        absorb(c.sink[hq] * kLog2e, vz, false);
+        absorb(sink_v * kLog2e, vz, false);
       }
       if (col_ok) {
         const float vdeq = c.v_deq ? c.v_deq[cur.h] : 1.0f;
@@ -1006,12 +1084,12 @@ MIA_DEV void split_body(const P &c) {
 
 template <int D, int NCP, bool FP8, bool PK>
 __global__ __launch_bounds__(256, wg_per_cu(D, FP8)) void decode_split_kernel(DecodeKParams p) {
-  split_body<D, NCP, FP8, PK, false>(p);
+  split_body<D, NCP, FP8, PK, false, kWaves>(p);
 }
 
-template <int D, int NCP, bool FP8, bool PK>
-__global__ __launch_bounds__(one_waves(D) * 64) void decode_onepass_kernel(CombineParams c) {
-  split_body<D, NCP, FP8, PK, true>(c);
+template <int D, int NCP, bool FP8, bool PK, int OW>
+__global__ __launch_bounds__(OW * 64) void decode_onepass_kernel(CombineParams c) {
+  split_body<D, NCP, FP8, PK, true, OW>(c);
 }
 
 // ---------------------------------------------------------------------------
@@ -1219,15 +1297,20 @@ void launch_split_ncp(int ncp, const DecodeKParams &kp, dim3 grid,
   else launch_split<D, 16, FP8, PK>(kp, grid, s);
 }
 
-// one-pass kernel: one workgroup of one_waves(D) waves per (row, kv head) segment
+// one-pass kernel: one workgroup of ow waves per (row, kv head) segment
+template <int D, bool FP8, int OW, bool PK>
+void launch_onepass_ow(int ncp, const CombineParams &cp, dim3 grid, hipStream_t s) {
+  if (ncp <= 4)
+    hipLaunchKernelGGL((decode_onepass_kernel<D, 4, FP8, PK, OW>), grid, dim3(OW * 64), 0, s, cp);
+  else if (ncp <= 8)
+    hipLaunchKernelGGL((decode_onepass_kernel<D, 8, FP8, PK, OW>), grid, dim3(OW * 64), 0, s, cp);
+  else
+    hipLaunchKernelGGL((decode_onepass_kernel<D, 16, FP8, PK, OW>), grid, dim3(OW * 64), 0, s, cp);
+}
+
 template <int D, bool FP8, bool PK = false>
 void launch_onepass_ncp(int ncp, const CombineParams &cp, dim3 grid, hipStream_t s) {
-  if (ncp <= 4)
-    hipLaunchKernelGGL((decode_onepass_kernel<D, 4, FP8, PK>), grid, dim3(one_waves(D) * 64), 0, s, cp);
-  else if (ncp <= 8)
-    hipLaunchKernelGGL((decode_onepass_kernel<D, 8, FP8, PK>), grid, dim3(one_waves(D) * 64), 0, s, cp);
-  else
-    hipLaunchKernelGGL((decode_onepass_kernel<D, 16, FP8, PK>), grid, dim3(one_waves(D) * 64), 0, s, cp);
+  launch_onepass_ow<D, FP8, one_waves(D), PK>(ncp, cp, grid, s);
 }
 
 }  // namespace
@@ -1299,11 +1382,14 @@ DecodePlan plan_decode(const mia_decode_args &a) {
   const bool flat_new =
       a.batch <= 1 || (a.k_new_stride[0] == (int64_t)a.s_active * a.k_new_stride[1] &&
                        a.v_new_stride[0] == (int64_t)a.s_active * a.v_new_stride[1]);
+  // With private write slots (a.write_private) the one-pass kernel writes
+  // the rows itself, after its own reads, and needs no scatter launch.
+  const bool no_scatter = a.write_slots == nullptr || a.write_private;
   const bool short_tab =
       t_max <= kOnePassTiles ||
-      (t_max <= kOnePassTilesFew && a.write_slots == nullptr &&
+      (t_max <= kOnePassTilesFew && no_scatter &&
        (int64_t)a.batch * a.num_kv_heads <= device_cu_count());
-  pl.one_pass = a.split_tokens == 0 && short_tab && (a.write_slots == nullptr || flat_new);
+  pl.one_pass = a.split_tokens == 0 && short_tab && (no_scatter || flat_new);
   const size_t rows = (size_t)a.batch * a.num_kv_heads * pl.num_splits * pl.ncols;
   size_t o_bytes = rows * (size_t)a.head_dim * sizeof(float);
   o_bytes = (o_bytes + 255) & ~(size_t)255;
@@ -1389,6 +1475,7 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
 
   kp.col0 = 0;
   CombineParams cp;
+  cp.onepass_write = 0;
   cp.k = kp;
   cp.k_new = (const uint16_t *)a.k_new;
   cp.v_new = (const uint16_t *)a.v_new;
@@ -1425,8 +1512,10 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
       if (rc) return rc;
     }
     const dim3 ogrid((unsigned)(a.batch * a.num_kv_heads));
+    const bool fused_write = a.write_slots && a.write_private;
     for (int cg = 0; cg < pl.col_groups; ++cg) {
       cp.k.col0 = cg * 16;
+      cp.onepass_write = fused_write && cg == 0;  // one column group writes the rows
       const int ncp = std::min(16, pl.ncols - cp.k.col0);
       if (a.head_dim == 128) {
         if (a.k_packed) launch_onepass_ncp<128, true, true>(ncp, cp, ogrid, s);
@@ -1445,7 +1534,7 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
                          "decode: timing event");
       if (rc) return rc;
     }
-    if (!a.write_slots) return MIA_OK;
+    if (!a.write_slots || fused_write) return MIA_OK;
     // the active rows of the batch as one token sequence (t = b * S + s)
     mia_kv_write_args w{};
     w.k_src = a.k_new;

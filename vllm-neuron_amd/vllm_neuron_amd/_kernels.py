@@ -248,13 +248,16 @@ def paged_decode(
     write_slots: Optional[torch.Tensor] = None,
     k_packed: bool = False,
     no_alloc: bool = False,
+    write_private: bool = False,
 ) -> torch.Tensor:
     """Attention of ``q [B, S, Hq, d]`` over the paged prior context plus the
     active rows ``k_new/v_new [B, S, Hkv, d]``; returns ``[B, S, Hq, d]`` bf16.
 
     ``write_slots [B, S]`` (int32/int64) fuses the cache update: the active
     rows are written to those slots after attention has read the cache;
-    slots outside the pool are skipped.  ``k_packed``: ``k_cache`` is the
+    slots outside the pool are skipped.  ``write_private``: no row attends
+    to another row's write slot, so each row may be written right after its
+    own reads (the short-table kernel then writes them itself).  ``k_packed``: ``k_cache`` is the
     packed FP8 layout ``[nb, Hkv, bs/2, d, 2]``, read as it lies.
     ``no_alloc``: launch through ``mia_paged_decode_noalloc``, whose split-K
     scratch is the library's static per-device array (``workspace`` is
@@ -371,6 +374,7 @@ def paged_decode(
         write_slots = write_slots.contiguous()
         a.write_slots = write_slots.data_ptr()
         a.write_slot_dtype = N.mia_dtype(write_slots.dtype)
+        a.write_private = 1 if write_private else 0
     L = N.lib()
     if no_alloc:
         N.check(L.mia_paged_decode_noalloc(ctypes.byref(a), N.stream_ptr(dev)),

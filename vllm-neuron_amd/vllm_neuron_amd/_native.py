@@ -99,7 +99,7 @@ class DecodeArgs(ctypes.Structure):
         ("workspace", c_vp), ("workspace_bytes", ctypes.c_size_t),
         ("split_tokens", c_i32), ("_pad1", c_i32),
         ("split_event_begin", c_vp), ("split_event_end", c_vp),
-        ("write_slots", c_vp), ("write_slot_dtype", c_i32), ("_pad2", c_i32),
+        ("write_slots", c_vp), ("write_slot_dtype", c_i32), ("write_private", c_i32),
     ]
 
 

@@ -180,6 +180,7 @@ def attention_decode(
     *,
     k_dequant_scale: Optional[Tensor] = None,
     v_dequant_scale: Optional[Tensor] = None,
+    kv_cache_update_private: bool = False,
 ):
     """Fused attention block for token generation.
 
@@ -187,6 +188,10 @@ def attention_decode(
     ``(output, K_out [d, B*Hkv, S_tkg], V_out [B, Hkv, S_tkg, d])``.
     ``output`` is ``[B*S_tkg, H]`` with ``W_out`` else ``[B, q_heads, d,
     S_tkg]``.  See the module docstring for the split of work.
+    ``kv_cache_update_private`` (not in the reference): the caller states
+    that no row attends to another row's ``kv_cache_update_idx`` slot, as
+    vLLM's block ownership gives; short tables then write the cache in the
+    attention kernel instead of a separate launch after it.
     """
     # ---- validation, in the reference's order (attention_decode.py:1484-1575)
     if dcp_size > 1 and dcp_group is None:
@@ -304,6 +309,7 @@ def attention_decode(
         k_scale=k_scale, v_scale=v_scale, fp8_packed=fp8_packed,
         k_dequant_scale=k_dequant_scale, v_dequant_scale=v_dequant_scale,
         write_slots=kv_cache_update_idx if fuse_write else None,
+        write_slots_private=kv_cache_update_private,
     )  # [B, S, Hq, d]
 
     # ---- stage 8: KV cache update (HIP; fused above unless update_cache is off)
@@ -357,12 +363,16 @@ def paged_decode_core(
     split_tokens: int = 0,
     split_events: Optional[tuple] = None,
     write_slots: Optional[Tensor] = None,
+    write_slots_private: bool = False,
 ) -> Tensor:
     """Attention core of stages 7a-7g: ``q [B, S, Hq, d]`` attends to the
     paged prior context and the active rows ``k_new/v_new [B, S, Hkv, d]``
     (placed at the last S slots of the context, as the reference does).
     ``write_slots [B*S]`` fuses stage 8 (the cache update) into the same
-    launch sequence.  Returns ``[B, S, Hq, d]`` bf16."""
+    launch sequence; ``write_slots_private`` states that no row attends to
+    another row's write slot (vLLM's block ownership), which lets a row's
+    rows be written right after that row's reads.  Returns ``[B, S, Hq, d]``
+    bf16."""
     B, S, Hq, d = q.shape
     kv_heads = k_new.shape[2]
     fp8 = K_cache.dtype == torch.float8_e4m3fn
@@ -374,7 +384,8 @@ def paged_decode_core(
     kw = dict(softmax_scale=softmax_scale, sink=sink,
               k_dequant=k_dequant_scale, v_dequant=v_dequant_scale,
               workspace=workspace, split_tokens=split_tokens, split_events=split_events,
-              write_slots=write_slots, k_packed=fp8_packed)
+              write_slots=write_slots, k_packed=fp8_packed,
+              write_private=bool(write_slots_private))
     if k_scale is not None:
         kw["quant_mode"] = _quant_mode_for(k_new.dtype, k_scale)
         kw["k_quant"] = k_scale

@@ -212,14 +212,15 @@ def swa_trim(block_table, ctx_lens, num_swa_blocks: int, block_size: int):
 def _decode_launch(q, k_new, v_new, k_cache, v_cache, block_table, out, workspace, pos_ids,
                    start_pos, active_mask, full_mask, sink, k_dequant, v_dequant, k_quant,
                    v_quant, write_slots, softmax_scale, mask_block_len, quant_mode,
-                   quant_per_head, split_tokens, k_packed, no_alloc) -> None:
+                   quant_per_head, split_tokens, k_packed, no_alloc,
+                   write_private=False) -> None:
     K.paged_decode(q, k_new, v_new, k_cache, v_cache, block_table, softmax_scale=softmax_scale,
                    pos_ids=pos_ids, start_pos=start_pos, active_mask=active_mask,
                    full_mask=full_mask, mask_block_len=mask_block_len, sink=sink,
                    k_dequant=k_dequant, v_dequant=v_dequant, quant_mode=quant_mode,
                    k_quant=k_quant, v_quant=v_quant, quant_per_head=quant_per_head, out=out,
                    workspace=workspace, split_tokens=split_tokens, write_slots=write_slots,
-                   k_packed=k_packed, no_alloc=no_alloc)
+                   k_packed=k_packed, no_alloc=no_alloc, write_private=write_private)
 
 
 # Two ops for one kernel pair: the attention alone reads the caches
@@ -258,18 +259,18 @@ def _paged_decode_write(q: Tensor, k_new: Tensor, v_new: Tensor, k_cache: Tensor
                         k_quant: Optional[Tensor], v_quant: Optional[Tensor],
                         write_slots: Tensor, softmax_scale: float, mask_block_len: int,
                         quant_mode: int, quant_per_head: bool, split_tokens: int,
-                        k_packed: bool, no_alloc: bool) -> None:
+                        k_packed: bool, no_alloc: bool, write_private: bool) -> None:
     _decode_launch(q, k_new, v_new, k_cache, v_cache, block_table, out, workspace, pos_ids,
                    start_pos, active_mask, full_mask, sink, k_dequant, v_dequant, k_quant,
                    v_quant, write_slots, softmax_scale, mask_block_len, quant_mode,
-                   quant_per_head, split_tokens, k_packed, no_alloc)
+                   quant_per_head, split_tokens, k_packed, no_alloc, write_private)
 
 
 @_paged_decode_write.register_fake
 def _(q, k_new, v_new, k_cache, v_cache, block_table, out, workspace, pos_ids, start_pos,
       active_mask, full_mask, sink, k_dequant, v_dequant, k_quant, v_quant, write_slots,
       softmax_scale, mask_block_len, quant_mode, quant_per_head, split_tokens, k_packed,
-      no_alloc):
+      no_alloc, write_private):
     return None
 
 
@@ -279,7 +280,7 @@ def paged_decode(q, k_new, v_new, k_cache, v_cache, block_table, *, softmax_scal
                  quant_mode: int = N.QUANT_NONE, k_quant=None, v_quant=None,
                  quant_per_head: bool = False, out=None, workspace=None, split_tokens: int = 0,
                  split_events=None, write_slots=None, k_packed: bool = False,
-                 no_alloc: bool = False) -> Tensor:
+                 no_alloc: bool = False, write_private: bool = False) -> Tensor:
     """``_kernels.paged_decode`` through ``mia::paged_decode`` (no cache
     write) or ``mia::paged_decode_write`` (with ``write_slots``);
     ``split_events`` (timing instrumentation, eager only) calls the kernel
@@ -293,7 +294,8 @@ def paged_decode(q, k_new, v_new, k_cache, v_cache, block_table, *, softmax_scal
                               v_quant=v_quant, quant_per_head=quant_per_head, out=out,
                               workspace=workspace, split_tokens=split_tokens,
                               split_events=split_events, write_slots=write_slots,
-                              k_packed=k_packed, no_alloc=no_alloc)
+                              k_packed=k_packed, no_alloc=no_alloc,
+                              write_private=write_private)
     if out is None:
         out = q.new_empty(q.shape, dtype=torch.bfloat16)
     common = (q, k_new, v_new, k_cache, v_cache, block_table, out, workspace, pos_ids, start_pos,
@@ -303,7 +305,7 @@ def paged_decode(q, k_new, v_new, k_cache, v_cache, block_table, *, softmax_scal
     if write_slots is None:
         _paged_decode(*common, *scal)
     else:
-        _paged_decode_write(*common, write_slots, *scal)
+        _paged_decode_write(*common, write_slots, *scal, bool(write_private))
     return out
 
 
