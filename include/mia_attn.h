@@ -140,7 +140,13 @@ typedef struct {
   int32_t block_size;
   int32_t head_dim;
   int32_t num_blocks; /* physical blocks in the pool: ids are clamped to [0, num_blocks) */
-  void *out; /* [batch, num_kv_heads, blocks_per_seq*block_size, head_dim] */
+  void *out; /* [batch, num_kv_heads, blocks_per_seq*block_size, out_dim] */
+  /* Row width of `out` (0 = head_dim): out_dim > head_dim zero-pads every
+   * row (a multiple of 8).  The padded gather stages a cache of a head_dim
+   * the attention kernels do not take (not 64 or 128) as one they do; it is
+   * a copy of the gathered blocks in the cache dtype, zeros appended. */
+  int32_t out_dim;
+  int32_t _pad0;
 } mia_gather_args;
 
 int mia_gather_kv(const mia_gather_args *args, mia_stream_t stream);

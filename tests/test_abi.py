@@ -307,3 +307,16 @@ def test_one_pass_plan_needs_no_split_scratch():
     assert 0 < L.mia_decode_workspace_bytes(ctypes.byref(a)) <= 4096
     big = _decode_args(batch=1024, blocks_per_seq=16, s_active=2, num_q_heads=64, num_kv_heads=8)
     assert L.mia_decode_workspace_bytes(ctypes.byref(big)) > N.DECODE_NOALLOC_SCRATCH_BYTES
+
+
+def test_padded_gather_validation():
+    """The padded gather (rows zero-padded to out_dim) takes a larger
+    multiple of 8, bf16 or fp8 only."""
+    L = N.lib()
+    for od, text in ((100, "out_dim"), (64, "out_dim")):
+        a = _gather_args(head_dim=96, out_dim=od)
+        with pytest.raises(ValueError, match=text):
+            N.check(L.mia_gather_kv(ctypes.byref(a), None), "gather_kv")
+    a = _gather_args(head_dim=96, out_dim=128, cache_dtype=N.DTYPE_F32)
+    with pytest.raises(NotImplementedError, match="padded"):
+        N.check(L.mia_gather_kv(ctypes.byref(a), None), "gather_kv")

@@ -476,3 +476,42 @@ def test_one_pass_long_tables(gpu, case, S):
     assert (one.double() - ref).abs().max().item() <= tol
     assert (split.double() - ref).abs().max().item() <= tol
     assert (one - split).abs().max().item() <= (3e-2 if cfg.fp8 else 1.6e-2)
+
+
+@pytest.mark.parametrize("d,extra", [(80, {}), (96, dict(sink=True)), (112, dict(fp8=True)),
+                                     (96, dict(fp8=True, block_size=64)), (32, {}),
+                                     (80, dict(window=64, max_model_len=512, sink=True))])
+def test_head_dims_other_than_64_and_128(gpu, d, extra):
+    """Head dims the kernels do not take directly (the reference's torch
+    path takes any d; attention_decode.py:910-1037): the table's blocks are
+    staged once into rows zero-padded to 64 / 128.  Against float64 math,
+    one and three active tokens, with the fused cache write landing in the
+    caller's (unpadded) cache exactly as the standalone scatter writes it."""
+    from vllm_neuron_amd import _kernels as K
+    cfg = _small_cfg(**dict(dict(q_heads=16, kv_heads=2, head_dim=d, block_size=32,
+                                 ctx_lo=20, ctx_hi=900), **extra))
+    for S in (1, 3):
+        b = _make(cfg, gpu, S=S)
+        if b.start is not None:
+            b.start = torch.clamp(b.pos - cfg.window + 1, min=0)
+        B, Hkv = cfg.batch, cfg.kv_heads
+        nb, bs = b.k_cache.shape[0], cfg.block_size
+        g = torch.Generator().manual_seed(13)
+        slots = torch.randperm(nb * bs, generator=g)[:B * S].to(torch.int64).to(gpu)
+        kc, vc = b.k_cache.clone(), b.v_cache.clone()
+        ref = _fp32(b, d ** -0.5)              # the cache as the call reads it
+        out = _run_core(b, write_slots=slots)
+        assert out.shape == (B, S, cfg.q_heads, d)
+        err = (out.float().cpu().double() - ref).abs().max().item()
+        assert err <= (TOL_FP8 if cfg.fp8 else TOL_BF16), (S, err)
+        kw = {}
+        if cfg.fp8:
+            from vllm_neuron_amd.functional.attention.attention_decode import (
+                _quant_mode_for, _scale_per_head)
+            kw = dict(quant_mode=_quant_mode_for(b.k_new.dtype, b.k_quant), k_scale=b.k_quant,
+                      v_scale=b.v_quant, scale_per_head=_scale_per_head(b.k_quant, Hkv))
+        K.kv_write(b.k_new.reshape(B * S, Hkv, -1), b.v_new.reshape(B * S, Hkv, -1), slots,
+                   kc, vc, **kw)
+        torch.cuda.synchronize()
+        assert torch.equal(b.k_cache.view(torch.uint8), kc.view(torch.uint8))
+        assert torch.equal(b.v_cache.view(torch.uint8), vc.view(torch.uint8))

@@ -27,6 +27,10 @@ PREFILL_CASES = [
     (16, 2, 64, 32, 160, 96, 64, True, True, True),
     (4, 4, 128, 16, 33, 48, 0, False, True, False),
     (8, 1, 64, 32, 257, 512, 128, False, True, False),
+    # head dims staged through zero-padded rows (attention_segmented_cte.py:783-790: d <= 128)
+    (8, 2, 80, 32, 130, 64, 0, False, True, False),
+    (12, 2, 96, 16, 200, 128, 64, True, False, True),
+    (4, 4, 48, 32, 96, 32, 0, False, True, False),
 ]
 
 
@@ -80,14 +84,17 @@ def test_varlen_matches_per_sequence(gpu):
         assert err <= TOL_BF16, (i, err)
 
 
-def test_fp8_prefill_per_head_scales(gpu):
-    cfg = W.PrefillConfig("t", 1, 12, 2, 128, 64, 160, 128, 128, fp8=True, seed=77)
+@pytest.mark.parametrize("d,packed", [(128, False), (96, False), (96, True)])
+def test_fp8_prefill_per_head_scales(gpu, d, packed):
+    from vllm_neuron_amd.functional.attention.attention_decode import _swizzle_packed_k
+    cfg = W.PrefillConfig("t", 1, 12, 2, d, 64, 160, 128, 128, fp8=True, seed=77)
     b = W.make_prefill_batch(cfg, gpu)
     K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache, quant_mode=2,
                k_scale=b.k_quant, v_scale=b.v_quant, scale_per_head=True)
     q = b.q.transpose(0, 1).contiguous()
-    out = segmented_attention(q, b.k_cache, b.v_cache, b.block_table, b.prior.view(1, 1),
-                              cfg.block_size, 0, k_dequant_scale=b.k_dequant,
+    kc_in = _swizzle_packed_k(b.k_cache) if packed else b.k_cache
+    out = segmented_attention(q, kc_in, b.v_cache, b.block_table, b.prior.view(1, 1),
+                              cfg.block_size, 0, fp8_packed=packed, k_dequant_scale=b.k_dequant,
                               v_dequant_scale=b.v_dequant)
     # oracle: the reference semantics once per kv head with scalar folding
     # (scale * s_k[h], output * s_v[h])

@@ -106,6 +106,12 @@ int mia_gather_kv(const mia_gather_args *a, mia_stream_t stream) {
   MIA_REQUIRE(a->batch >= 0 && a->num_kv_heads > 0 && a->blocks_per_seq >= 0 &&
                   a->block_size > 0 && a->head_dim > 0 && a->num_blocks > 0,
               MIA_ERR_VALUE, "gather: bad geometry");
+  MIA_REQUIRE(a->out_dim == 0 || a->out_dim == a->head_dim ||
+                  (a->out_dim > a->head_dim && a->out_dim % 8 == 0),
+              MIA_ERR_VALUE, "gather: out_dim must be 0, head_dim, or a larger multiple of 8");
+  MIA_REQUIRE(a->out_dim == 0 || a->out_dim == a->head_dim ||
+                  a->cache_dtype == MIA_DTYPE_BF16 || a->cache_dtype == MIA_DTYPE_FP8_E4M3FN,
+              MIA_ERR_NOT_IMPLEMENTED, "gather: padded rows of bf16 or fp8 caches only");
   return mia::launch_gather(*a, (hipStream_t)stream);
 }
 

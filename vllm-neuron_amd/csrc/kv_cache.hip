@@ -10,6 +10,8 @@
 //                     zero tail and head-dim padding, layout transpose)
 // All are HBM-bound element kernels; each thread owns whole 16-byte chunks
 // where the layout allows it.
+#include <type_traits>
+
 #include "mia_device.h"
 #include "mia_internal.h"
 
@@ -156,7 +158,7 @@ __global__ __launch_bounds__(256) void kv_write_vec_kernel(mia_kv_write_args a, 
   }
 }
 
-MIA_DEV int elem_bytes(int dtype) {
+__host__ __device__ inline int elem_bytes(int dtype) {
   return dtype == MIA_DTYPE_FP8_E4M3FN ? 1 : (dtype == MIA_DTYPE_F32 ? 4 : 2);
 }
 
@@ -190,6 +192,50 @@ __global__ void gather_kernel(mia_gather_args a, int64_t total) {
   if (eb == 1) ((uint8_t *)a.out)[i] = ((const uint8_t *)a.cache)[src];
   else if (eb == 2) ((uint16_t *)a.out)[i] = ((const uint16_t *)a.cache)[src];
   else ((uint32_t *)a.out)[i] = ((const uint32_t *)a.cache)[src];
+}
+
+// Padded gather: one workgroup per (row b, kv head h, table entry j) block;
+// thread (t, u) writes elements [8u, 8u + 8) of token row t of the output
+// row of width out_dim, zeros past head_dim.  VEC: the source rows are
+// contiguous, start 16-byte (bf16) / 8-byte (fp8) aligned and head_dim is a
+// multiple of 8, so a unit is one load.
+template <typename T, bool VEC>
+__global__ __launch_bounds__(256) void gather_pad_kernel(mia_gather_args a) {
+  typedef typename std::conditional<sizeof(T) == 2, u32x4_t, u32x2_t>::type unit_t;
+  const int64_t bid = blockIdx.x;  // (b * Hkv + h) * nblk + j
+  const int j = (int)(bid % a.blocks_per_seq);
+  const int64_t bh = bid / a.blocks_per_seq;
+  const int h = (int)(bh % a.num_kv_heads);
+  const int64_t b = bh / a.num_kv_heads;
+  int32_t blk = a.block_table[b * a.bt_stride[0] + h * a.bt_stride[1] + j * a.bt_stride[2]];
+  blk = blk < 0 ? 0 : (blk >= a.num_blocks ? a.num_blocks - 1 : blk);
+  const int upr = a.out_dim / 8;  // units per row
+  const T *src = (const T *)a.cache;
+  T *dst = (T *)a.out + bid * a.block_size * (int64_t)a.out_dim;
+  for (int i = threadIdx.x; i < a.block_size * upr; i += 256) {
+    const int t = i / upr, u = i - t * upr, e0 = 8 * u;
+    unit_t w;
+    if (VEC && e0 + 8 <= a.head_dim) {
+      const int64_t o = blk * a.cache_stride[0] + h * a.cache_stride[1] + t * a.cache_stride[2] + e0;
+      w = *reinterpret_cast<const unit_t *>(src + o);
+    } else {
+      T v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int e = e0 + k;
+        int64_t o;
+        if (a.k_packed)
+          o = blk * a.cache_stride[0] + h * a.cache_stride[1] + (t >> 1) * a.cache_stride[2] +
+              e * a.cache_stride[3] + (t & 1) * a.cache_stride[4];
+        else
+          o = blk * a.cache_stride[0] + h * a.cache_stride[1] + t * a.cache_stride[2] +
+              e * a.cache_stride[3];
+        v[k] = e < a.head_dim ? src[o] : (T)0;
+      }
+      w = __builtin_bit_cast(unit_t, v);
+    }
+    *reinterpret_cast<unit_t *>(dst + (int64_t)t * a.out_dim + e0) = w;
+  }
 }
 
 // Packed K permutation on contiguous tensors.
@@ -481,6 +527,23 @@ int launch_kv_write(const mia_kv_write_args &a, hipStream_t s) {
 }
 
 int launch_gather(const mia_gather_args &a, hipStream_t s) {
+  if (a.out_dim != 0 && a.out_dim != a.head_dim) {
+    const int64_t nblocks = (int64_t)a.batch * a.num_kv_heads * a.blocks_per_seq;
+    if (nblocks == 0) return MIA_OK;
+    const int eb = elem_bytes(a.cache_dtype);
+    const bool vec = !a.k_packed && a.cache_stride[3] == 1 && a.head_dim % 8 == 0 &&
+                     ((uintptr_t)a.cache % (8 * eb)) == 0 && (a.cache_stride[0] * eb) % (8 * eb) == 0 &&
+                     (a.cache_stride[1] * eb) % (8 * eb) == 0 && (a.cache_stride[2] * eb) % (8 * eb) == 0;
+    const dim3 g((unsigned)nblocks);
+    if (eb == 2) {
+      if (vec) hipLaunchKernelGGL((gather_pad_kernel<uint16_t, true>), g, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((gather_pad_kernel<uint16_t, false>), g, dim3(256), 0, s, a);
+    } else {
+      if (vec) hipLaunchKernelGGL((gather_pad_kernel<uint8_t, true>), g, dim3(256), 0, s, a);
+      else hipLaunchKernelGGL((gather_pad_kernel<uint8_t, false>), g, dim3(256), 0, s, a);
+    }
+    return check_hip(hipGetLastError(), "padded gather launch");
+  }
   const int64_t total = (int64_t)a.batch * a.num_kv_heads * a.blocks_per_seq *
                         a.block_size * a.head_dim;
   if (total == 0) return MIA_OK;

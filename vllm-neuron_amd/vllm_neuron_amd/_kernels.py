@@ -134,8 +134,10 @@ def kv_write(
 # ---------------------------------------------------------------------------
 # gather (parity / debug)
 # ---------------------------------------------------------------------------
-def gather_kv(cache: torch.Tensor, block_table: torch.Tensor, *, k_packed: bool = False) -> torch.Tensor:
-    """[B, Hkv, nblk*bs, d] (cache dtype) gathered through the block table."""
+def gather_kv(cache: torch.Tensor, block_table: torch.Tensor, *, k_packed: bool = False,
+              out_dim: int = 0) -> torch.Tensor:
+    """[B, Hkv, nblk*bs, d] (cache dtype) gathered through the block table;
+    with ``out_dim > d`` each row is zero-padded to ``out_dim``."""
     dev = N.require_gpu(cache, block_table)
     if block_table.dtype != torch.int32:
         raise ValueError("block table must be int32")
@@ -150,7 +152,8 @@ def gather_kv(cache: torch.Tensor, block_table: torch.Tensor, *, k_packed: bool 
         bts = [block_table.stride(0), block_table.stride(1) if th > 1 else 0, block_table.stride(2)]
     else:
         raise ValueError("block table must be 2D or 3D")
-    out = torch.empty((B, hkv, nblk * bs, d), dtype=cache.dtype, device=dev)
+    od = int(out_dim) if out_dim else d
+    out = torch.empty((B, hkv, nblk * bs, od), dtype=cache.dtype, device=dev)
     a = N.GatherArgs()
     a.cache = cache.data_ptr()
     a.cache_dtype = N.mia_dtype(cache.dtype)
@@ -165,6 +168,7 @@ def gather_kv(cache: torch.Tensor, block_table: torch.Tensor, *, k_packed: bool 
     a.head_dim = d
     a.num_blocks = nb
     a.out = out.data_ptr()
+    a.out_dim = od
     N.check(N.lib().mia_gather_kv(ctypes.byref(a), N.stream_ptr(dev)), "gather_kv")
     return out
 

@@ -69,6 +69,7 @@ class GatherArgs(ctypes.Structure):
         ("cache_stride", c_i64 * 5), ("block_table", c_vp), ("bt_stride", c_i64 * 3),
         ("batch", c_i32), ("num_kv_heads", c_i32), ("blocks_per_seq", c_i32),
         ("block_size", c_i32), ("head_dim", c_i32), ("num_blocks", c_i32), ("out", c_vp),
+        ("out_dim", c_i32), ("_pad0", c_i32),
     ]
 
 

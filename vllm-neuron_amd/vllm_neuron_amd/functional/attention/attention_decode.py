@@ -380,6 +380,14 @@ def paged_decode_core(
         raise NotImplementedError("k_scale/v_scale are only meaningful with an fp8 KV cache")
     if fp8 and V_cache.dtype != K_cache.dtype:
         raise ValueError("K and V caches must share a dtype")
+    if d not in (64, 128):
+        return _padded_head_dim_decode(
+            q, k_new, v_new, K_cache, V_cache, block_table, block_len=block_len,
+            attention_mask=attention_mask, pos_ids=pos_ids,
+            swa_start_pos_ids=swa_start_pos_ids, sink=sink, softmax_scale=softmax_scale,
+            k_scale=k_scale, v_scale=v_scale, fp8_packed=fp8_packed,
+            k_dequant_scale=k_dequant_scale, v_dequant_scale=v_dequant_scale,
+            workspace=workspace, split_tokens=split_tokens, write_slots=write_slots)
 
     kw = dict(softmax_scale=softmax_scale, sink=sink,
               k_dequant=k_dequant_scale, v_dequant=v_dequant_scale,
@@ -413,6 +421,51 @@ def paged_decode_core(
             kw["full_mask"] = attention_mask
             kw["mask_block_len"] = _mask_resize_block_len(block_len, B, Hq, S, S_ctx)
     return K.paged_decode(q, k_new, v_new, K_cache, V_cache, block_table, **kw)
+
+
+def _staged_paged(rows: Tensor, nblk: int, bs: int) -> Tensor:
+    """A padded gather ``[B, Hkv, nblk*bs, Dp]`` viewed as a paged cache
+    ``[nb', Hkv, bs, Dp]`` whose block ``b*Hkv*nblk + j`` is table entry j of
+    row b (head h at ``h*nblk*bs*Dp`` past it)."""
+    B, Hkv, _, Dp = rows.shape
+    nb = (B - 1) * Hkv * nblk + nblk
+    return torch.as_strided(rows, (nb, Hkv, bs, Dp), (bs * Dp, nblk * bs * Dp, Dp, 1))
+
+
+def _padded_head_dim_decode(q, k_new, v_new, K_cache, V_cache, block_table, *, block_len,
+                            attention_mask, pos_ids, swa_start_pos_ids, sink, softmax_scale,
+                            k_scale, v_scale, fp8_packed, k_dequant_scale, v_dequant_scale,
+                            workspace, split_tokens, write_slots):
+    """Head dims other than 64 and 128 (a multiple of 8, at most 128; the
+    reference's torch path takes any, attention_decode.py:910-1037): the
+    blocks of every table row are gathered once into a copy whose rows are
+    zero-padded to 64 or 128 (``mia_gather_kv`` with out_dim), read through
+    a per-row block table, with q and the active rows padded the same way;
+    zero dims add nothing to q.k and their output columns are dropped.  The
+    cache update then goes to the caller's cache in the reference's order
+    (after every read)."""
+    B, S, Hq, d = q.shape
+    kv_heads = k_new.shape[2]
+    if d > 128 or d % 8:
+        raise NotImplementedError("attention_decode: head_dim must be a multiple of 8, at most 128")
+    Dp = 64 if d <= 64 else 128
+    nblk = block_table.shape[-1]
+    kc = _staged_paged(K.gather_kv(K_cache, block_table, k_packed=fp8_packed, out_dim=Dp),
+                       nblk, block_len)
+    vc = _staged_paged(K.gather_kv(V_cache, block_table, out_dim=Dp), nblk, block_len)
+    base = torch.arange(B, dtype=torch.int32, device=q.device).view(B, 1) * (kv_heads * nblk)
+    table = base + torch.arange(nblk, dtype=torch.int32, device=q.device).view(1, nblk)
+    pad = lambda t: torch.nn.functional.pad(t, (0, Dp - d))
+    out = paged_decode_core(pad(q), pad(k_new), pad(v_new), kc, vc, table, block_len=block_len,
+                            S_ctx=nblk * block_len, attention_mask=attention_mask,
+                            pos_ids=pos_ids, swa_start_pos_ids=swa_start_pos_ids, sink=sink,
+                            softmax_scale=softmax_scale, k_scale=k_scale, v_scale=v_scale,
+                            k_dequant_scale=k_dequant_scale, v_dequant_scale=v_dequant_scale,
+                            workspace=workspace, split_tokens=split_tokens)
+    if write_slots is not None:
+        _write_rows(k_new.reshape(B * S, kv_heads, d), v_new.reshape(B * S, kv_heads, d),
+                    write_slots, K_cache, V_cache, k_scale, v_scale, kv_heads, fp8_packed)
+    return out[..., :d]
 
 
 def _write_rows(k_rows, v_rows, slots, K_cache, V_cache, k_scale, v_scale, kv_heads,

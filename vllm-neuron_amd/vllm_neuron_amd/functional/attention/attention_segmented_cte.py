@@ -11,7 +11,9 @@ fully-masked rows give 0.  The work runs in the HIP MFMA kernel
 
 The Trainium kernel's shape constraints (segment sizes from a fixed set,
 ``S_q == kv_segment_size``, ``head_dim <= 128``; :776-823) do not apply to
-the MI355X kernel and are not imposed; head_dim must be 64 or 128.
+the MI355X kernel and are not imposed; head_dim is any multiple of 8 up to
+128 (64 and 128 read in place, others through a zero-padded copy of the
+sequence's blocks).
 FP8 caches: the K dequant is folded into ``scale`` by the caller and the V
 dequant is applied by the caller, as in the reference (gpt_oss/model_bf16.py
 :699-727); ``k_scale``/``v_scale`` are accepted and ignored like the torch
@@ -87,12 +89,34 @@ def segmented_attention(
         raise ValueError(f"block_size {block_size} does not match the cache ({cache_bs})")
     if q.dtype != torch.bfloat16:
         raise NotImplementedError("segmented_attention: q must be bf16")
+    if D > _MAX_HEAD_DIM or D % 8:
+        raise NotImplementedError("segmented_attention: head_dim must be a multiple of 8, at "
+                                  "most 128")
     dev = q.device
+    table = block_tables[:1]
+    if D not in (64, 128):
+        # head dims the kernels do not take (attention_segmented_cte.py:783-790
+        # allows any d <= 128): the sequence's blocks gathered once into rows
+        # zero-padded to 64 or 128, read through an identity table; zero dims
+        # add nothing to q.k and their output columns are dropped
+        Dp = 64 if D <= 64 else 128
+        nblk = table.shape[-1]
+        stage = lambda c, pk: K.gather_kv(c, table, k_packed=pk, out_dim=Dp)[0]  # [Hkv, L, Dp]
+        as_paged = lambda r: torch.as_strided(r, (nblk, num_kv_heads, block_size, Dp),
+                                              (block_size * Dp, nblk * block_size * Dp, Dp, 1))
+        k_cache, v_cache = as_paged(stage(k_cache, fp8_packed)), as_paged(stage(v_cache, False))
+        fp8_packed = False
+        table = M.identity_table(dev, nblk)
+        out = segmented_attention(
+            torch.nn.functional.pad(q, (0, Dp - D)), k_cache, v_cache, table, prior_tokens,
+            block_size, kv_segment_size, scale, True, False, sliding_window, sink, False,
+            k_scale, v_scale, k_dequant_scale=k_dequant_scale, v_dequant_scale=v_dequant_scale)
+        out = out[..., :D]
+        return out.transpose(1, 2) if tp_out else out
     if q.stride(2) != 1 or (q.stride(0) * 2) % 16 or (q.stride(1) * 2) % 16:
         q = q.contiguous()
     cu = M.device_i32(dev, (0, S_q))   # made once per (device, S_q): no copy per call
     prior = prior_tokens.reshape(-1)[:1]
-    table = block_tables[:1]
     out = torch.empty((Nh, S_q, D), dtype=torch.bfloat16, device=dev)
     K.paged_prefill(
         q.transpose(0, 1),  # [S_q, Nh, D] view: token stride, head stride

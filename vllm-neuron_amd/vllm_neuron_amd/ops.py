@@ -62,12 +62,12 @@ def kv_write(k_src, v_src, slots, k_cache, v_cache, *, k_packed=False, quant_mod
 
 
 @custom_op("mia::gather_kv", mutates_args=())
-def _gather_kv(cache: Tensor, block_table: Tensor, k_packed: bool) -> Tensor:
-    return K.gather_kv(cache, block_table, k_packed=k_packed)
+def _gather_kv(cache: Tensor, block_table: Tensor, k_packed: bool, out_dim: int) -> Tensor:
+    return K.gather_kv(cache, block_table, k_packed=k_packed, out_dim=out_dim)
 
 
 @_gather_kv.register_fake
-def _(cache, block_table, k_packed):
+def _(cache, block_table, k_packed, out_dim):
     if k_packed:   # [nb, Hkv, bs/2, d, 2] or [nb, bs/2, d, 2]
         hkv = cache.shape[1] if cache.dim() == 5 else 1
         bs, d = cache.shape[-3] * 2, cache.shape[-2]
@@ -75,11 +75,11 @@ def _(cache, block_table, k_packed):
         hkv = cache.shape[1] if cache.dim() == 4 else 1
         bs, d = cache.shape[-2], cache.shape[-1]
     B, nblk = block_table.shape[0], block_table.shape[-1]
-    return cache.new_empty((B, hkv, nblk * bs, d))
+    return cache.new_empty((B, hkv, nblk * bs, out_dim or d))
 
 
-def gather_kv(cache, block_table, *, k_packed=False) -> Tensor:
-    return _gather_kv(cache, block_table, bool(k_packed))
+def gather_kv(cache, block_table, *, k_packed=False, out_dim: int = 0) -> Tensor:
+    return _gather_kv(cache, block_table, bool(k_packed), int(out_dim))
 
 
 @custom_op("mia::packed_k_convert", mutates_args=())
