@@ -46,6 +46,22 @@ for _p in (ROOT, ROOT / "vllm-neuron_amd"):
 HBM_PEAK_GBS = 8000.0        # MI355X HBM3E, GB/s
 BF16_PEAK_TFLOPS = 2500.0    # MI355X dense bf16 MFMA, TFLOP/s
 METRIC = "decode-attn KV GB/s (% of HBM peak) + prefill TFLOP/s at 8B shape, 1 GPU"
+SETTLE_S = 1.5               # idle before each secondary workload's timed replays
+
+
+def _warm(step, warmup: int, min_s: float = 0.1) -> None:
+    """``warmup`` untimed calls, and more until ``min_s`` seconds have
+    passed, so that the timed calls run at this workload's clocks."""
+    import torch
+
+    t_end = time.perf_counter() + min_s
+    n = 0
+    while n < warmup or time.perf_counter() < t_end:
+        step()
+        n += 1
+        if n % 16 == 0:
+            torch.cuda.synchronize()
+    torch.cuda.synchronize()
 
 
 def _decode_step_fn(b, dev):
@@ -77,9 +93,7 @@ def bench_decode(dev, steps, warmup):
     cfg = W.DECODE_CONFIGS["llama3_8b_decode_b64"]
     b = W.make_decode_batch(cfg, dev)
     step = _decode_step_fn(b, dev)
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
+    _warm(step, warmup)
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(steps)]
     for e0, e1 in ev:  # create the HIP events on this device/stream
@@ -129,9 +143,8 @@ def bench_prefill(dev, steps, warmup):
         K.paged_prefill(b.q, b.cu_seqlens, b.prior, b.max_seqlen_q, b.k_cache, b.v_cache,
                         b.block_table, scale=cfg.head_dim ** -0.5, out=out, workspace=ws)
 
-    for _ in range(warmup):
-        step()
-    torch.cuda.synchronize()
+    time.sleep(SETTLE_S)
+    _warm(step, warmup)
     # calls issued back to back between one event pair: the GPU time of a
     # call (attention + merge kernels), without host gaps between calls
     reps = 5
@@ -149,11 +162,15 @@ def bench_prefill(dev, steps, warmup):
     return dict(flops=flops, ms=ms, ms_med=ms, tflops=flops / (ms * 1e-3) / 1e12, batch=b)
 
 
-def _graph_us(fn, dev, reps: int, per_graph: int = 8) -> float:
+def _graph_us(fn, dev, reps: int, per_graph: int = 8, settle_s: float = 0.0) -> float:
     """GPU time of one ``fn()`` call: ``per_graph`` calls captured in one HIP
     graph, replayed ``reps`` times between one event pair (no per-call host
     launch cost in the timed region; the graph launch is amortised over
-    ``per_graph`` calls)."""
+    ``per_graph`` calls).  ``settle_s``: idle time, then ~100 ms of untimed
+    replays, before the timed ones, so that every workload is timed in the
+    same state (right after a sustained HBM stream the latency-bound
+    one-pass decode runs ~20 % slower for one to three seconds: Llama-3.2-1B
+    13.1 -> 15.7 us; straight after an idle the clocks are still ramping)."""
     import torch
 
     side = torch.cuda.Stream(device=dev)
@@ -169,6 +186,14 @@ def _graph_us(fn, dev, reps: int, per_graph: int = 8) -> float:
     for _ in range(2):
         graph.replay()
     torch.cuda.synchronize()
+    if settle_s > 0:
+        # idle, then the workload itself for ~100 ms so that the clocks are
+        # those of this workload, not of the one before it
+        time.sleep(settle_s)
+        t_end = time.perf_counter() + 0.1
+        while time.perf_counter() < t_end:
+            graph.replay()
+            torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record()
     for _ in range(reps):
@@ -215,7 +240,7 @@ def bench_secondary(dev, reps: int, cpu_rows: int = 0) -> dict:
                               softmax_scale=cfg.head_dim ** -0.5, workspace=ws,
                               write_slots=slots, write_slots_private=True, **kw)
 
-        us = _graph_us(step, dev, reps)
+        us = _graph_us(step, dev, reps, settle_s=SETTLE_S)
         nbytes = W.decode_bytes(b)
         gbs = nbytes / (us * 1e-6) / 1e9
         rec = {"us_per_call": round(us, 2), "algorithmic_bytes": nbytes, "GB_s": round(gbs, 1)}
@@ -240,7 +265,7 @@ def bench_secondary(dev, reps: int, cpu_rows: int = 0) -> dict:
                             b.block_table, scale=cfg.head_dim ** -0.5, k_dequant=b.k_dequant,
                             v_dequant=b.v_dequant, out=o, workspace=ws)
 
-        us = _graph_us(pstep, dev, reps)
+        us = _graph_us(pstep, dev, reps, settle_s=SETTLE_S)
         fl = W.prefill_flops(b)
         tf = fl / (us * 1e-6) / 1e12
         out[name] = {"us_per_call": round(us, 2), "flops": fl, "tflops": round(tf, 1),
@@ -262,7 +287,7 @@ def bench_secondary(dev, reps: int, cpu_rows: int = 0) -> dict:
             prefill_block_table=pb.block_table, max_seqlen_q=pb.max_seqlen_q,
             decode_workspace=dws, prefill_workspace=pws)
 
-    us = _graph_us(mstep, dev, reps)
+    us = _graph_us(mstep, dev, reps, settle_s=SETTLE_S)
     nbytes = W.decode_bytes(db) + W.prefill_bytes(pb)
     fl = W.prefill_flops(pb)
     floor_us = max(nbytes / (HBM_PEAK_GBS * 1e9), fl / (BF16_PEAK_TFLOPS * 1e12)) * 1e6

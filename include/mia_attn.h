@@ -360,7 +360,11 @@ typedef struct {
   int32_t non_causal;
   int32_t q_offset;
   int32_t empty_rows_uniform;
-  int32_t _pad3;
+  /* 0: the kernel is chosen from the shapes; 1: always the register-staged
+   * kernel (128 rows and 36 KB of LDS per workgroup), which fits on a CU
+   * beside a decode workgroup, for a prefill that runs concurrently with a
+   * decode (a mixed batch). */
+  int32_t compact_kernel;
 } mia_prefill_args;
 
 size_t mia_prefill_workspace_bytes(const mia_prefill_args *args);

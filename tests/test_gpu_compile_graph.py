@@ -141,7 +141,7 @@ def test_opcheck_registered_ops(gpu):
         torch.ops.mia.paged_prefill.default,
         (pb.q, pb.cu_seqlens, pb.prior, pb.k_cache, pb.v_cache, pb.block_table, pout, None,
          None, None, None, None, None, None, pb.max_seqlen_q, 0.125, 0, 0, False, 0, False,
-         False))
+         False, False))
     torch.library.opcheck(
         torch.ops.mia.kv_write.default,
         (pb.k_new, pb.v_new, pb.slots, pb.k_cache, pb.v_cache, False, 0, None, None, False))

@@ -1310,7 +1310,7 @@ bool use_dma_kernel(const mia_prefill_args &a) {
 
 PrefillPlan plan_prefill(const mia_prefill_args &a) {
   PrefillPlan pl;
-  pl.dma = use_dma_kernel(a);
+  pl.dma = !a.compact_kernel && use_dma_kernel(a);
   pl.rows_wg = pl.dma ? kDmaRows : kRowsWG;
   const int G = a.num_q_heads / a.num_kv_heads;
   pl.rows_max = a.max_seqlen_q * G;

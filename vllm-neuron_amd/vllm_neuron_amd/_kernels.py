@@ -425,6 +425,7 @@ def paged_prefill(
     bound_max: Optional[torch.Tensor] = None,
     empty_rows_uniform: bool = False,
     k_packed: bool = False,
+    compact_kernel: bool = False,
 ) -> torch.Tensor:
     """``q [T, Hq, d]`` (any token/head strides) over paged K/V; sequence i
     owns rows ``cu_seqlens_q[i]:cu_seqlens_q[i+1]`` and table row i.
@@ -534,6 +535,7 @@ def paged_prefill(
     a.non_causal = 1 if non_causal else 0
     a.q_offset = int(q_offset)
     a.empty_rows_uniform = 1 if empty_rows_uniform else 0
+    a.compact_kernel = 1 if compact_kernel else 0
     L = N.lib()
     need = L.mia_prefill_workspace_bytes(ctypes.byref(a))
     if need:

@@ -120,7 +120,7 @@ class PrefillArgs(ctypes.Structure):
         ("split_tokens", c_i32), ("_pad0", c_i32),
         ("kv_len", c_vp), ("bound_min", c_vp), ("bound_max", c_vp), ("bound_stride", c_i64 * 2),
         ("non_causal", c_i32), ("q_offset", c_i32), ("empty_rows_uniform", c_i32),
-        ("_pad3", c_i32),
+        ("compact_kernel", c_i32),
     ]
 
 

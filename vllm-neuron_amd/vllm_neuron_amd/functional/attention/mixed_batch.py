@@ -11,19 +11,23 @@ composition this function implements and is tested against:
     attention_decode.py:653-1182).
 
 Here the prefill sequences run as one varlen launch and the decode rows as
-one split-K launch, on the caller's stream, sharing the same paged cache;
-the decode rows' K/V are written to the cache by the decode's merge kernel
-(after every decode workgroup has read the cache), not by a separate
-scatter launch.
-The two launches run back to back: the decode is HBM-bound and needs every
-CU to approach the memory roofline (at the Llama-3-8B mixed shape its 60
-rows take 525 / 299 / 203 us on 64 / 128 / 256 CUs), and the two kernels
-run concurrently on complementary CU-masked streams measured 445-510 us
-against 295 us back to back, so the GPU is not split between them.  Two
-unmasked streams, with the decode at one or two workgroups per CU and the
-prefill on its copy-ring or its register-staged kernel (which fit beside a
-decode workgroup on a CU), took 320-372 us against 267-293 us back to
-back: the kernels slow each other down more than they overlap.
+one split-K launch, sharing the same paged cache; the decode rows' K/V are
+written to the cache by the decode's merge kernel (after every decode
+workgroup has read the cache), not by a separate scatter launch.
+
+The two halves run concurrently: the decode (HBM-bound, a persistent grid
+of one workgroup per CU) on a side stream that forks from and joins the
+caller's stream, the prefill's K/V write and attention on the caller's
+stream with the register-staged prefill kernel (36 KB of LDS, 128 rows per
+workgroup), which fits on each CU beside a decode workgroup, where the
+copy-ring kernel's 144 KB does not.  At the Llama-3-8B mixed shape: 247 us
+against 262-276 us back to back (decode alone 184 us, prefill alone 81-86
+us); raising the decode waves' issue priority (s_setprio) changed nothing,
+and the CU-masked split of the GPU between the halves was slower than
+either (the decode needs every CU's memory parallelism: 525 / 299 / 203 us
+on 64 / 128 / 256 CUs).  ``overlap=False`` runs them back to back on the
+caller's stream.  Requirement of the overlap (as in vLLM): the decode rows
+and the prefill sequences own disjoint cache blocks.
 """
 from __future__ import annotations
 
@@ -67,6 +71,7 @@ def mixed_batch_attention(
     v_dequant_scale: Optional[Tensor] = None,
     decode_workspace: Optional[Tensor] = None,
     prefill_workspace: Optional[Tensor] = None,
+    overlap: bool = True,
 ) -> Tuple[Optional[Tensor], Optional[Tensor]]:
     """Returns ``(out_decode [Bd, S_tkg, Hq, d], out_prefill [Tp, Hq, d])``."""
     d = V_cache.shape[-1]
@@ -79,6 +84,25 @@ def mixed_batch_attention(
                    v_scale=v_scale if v_scale is not None else k_scale,
                    scale_per_head=_scale_per_head(k_scale, kv_heads))
 
+    both = overlap and q_prefill is not None and q_decode is not None
+    out_d = None
+    side = None
+    if both:
+        dev = q_decode.device
+        side = _side_stream(dev)
+        cur = torch.cuda.current_stream(dev)
+        side.wait_stream(cur)
+    if q_decode is not None:
+        nblk = decode_block_table.shape[-1]
+        with torch.cuda.stream(side) if side is not None else _nullctx():
+            out_d = paged_decode_core(
+                q_decode, k_decode, v_decode, K_cache, V_cache, decode_block_table,
+                block_len=block_len, S_ctx=nblk * block_len, pos_ids=decode_pos_ids,
+                swa_start_pos_ids=decode_start_pos, sink=sink, softmax_scale=scale,
+                k_scale=k_scale, v_scale=v_scale, k_dequant_scale=k_dequant_scale,
+                v_dequant_scale=v_dequant_scale, workspace=decode_workspace,
+                write_slots=None if decode_slots is None else decode_slots.reshape(-1))
+
     out_p = None
     if q_prefill is not None:
         if k_prefill is not None:
@@ -87,16 +111,33 @@ def mixed_batch_attention(
             q_prefill, prefill_cu_seqlens, prefill_prior, max_seqlen_q,
             K_cache, V_cache, prefill_block_table, scale=scale,
             sliding_window=sliding_window, sink=sink,
-            k_dequant=k_dequant_scale, v_dequant=v_dequant_scale, workspace=prefill_workspace)
-
-    out_d = None
-    if q_decode is not None:
-        nblk = decode_block_table.shape[-1]
-        out_d = paged_decode_core(
-            q_decode, k_decode, v_decode, K_cache, V_cache, decode_block_table,
-            block_len=block_len, S_ctx=nblk * block_len, pos_ids=decode_pos_ids,
-            swa_start_pos_ids=decode_start_pos, sink=sink, softmax_scale=scale,
-            k_scale=k_scale, v_scale=v_scale, k_dequant_scale=k_dequant_scale,
-            v_dequant_scale=v_dequant_scale, workspace=decode_workspace,
-            write_slots=None if decode_slots is None else decode_slots.reshape(-1))
+            k_dequant=k_dequant_scale, v_dequant=v_dequant_scale, workspace=prefill_workspace,
+            compact_kernel=both)
+    if both:
+        cur.wait_stream(side)
+        # the decode output was allocated on the side stream and is used on
+        # the caller's (under capture the graph's private pool holds it)
+        if not torch.cuda.is_current_stream_capturing():
+            out_d.record_stream(cur)
     return out_d, out_p
+
+
+_SIDE: dict = {}
+
+
+def _side_stream(dev: torch.device) -> "torch.cuda.Stream":
+    """One side stream per device (default priority), made once."""
+    key = str(dev)
+    s = _SIDE.get(key)
+    if s is None:
+        s = torch.cuda.Stream(device=dev)
+        _SIDE[key] = s
+    return s
+
+
+class _nullctx:
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False

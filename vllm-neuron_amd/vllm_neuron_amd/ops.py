@@ -317,19 +317,20 @@ def _paged_prefill(q: Tensor, cu_seqlens_q: Tensor, prior_tokens: Tensor, k_cach
                    kv_len: Optional[Tensor], bound_min: Optional[Tensor],
                    bound_max: Optional[Tensor], max_seqlen_q: int, scale: float,
                    sliding_window: int, split_tokens: int, non_causal: bool, q_offset: int,
-                   empty_rows_uniform: bool, k_packed: bool) -> None:
+                   empty_rows_uniform: bool, k_packed: bool, compact_kernel: bool) -> None:
     K.paged_prefill(q, cu_seqlens_q, prior_tokens, max_seqlen_q, k_cache, v_cache, block_table,
                     scale=scale, sliding_window=sliding_window, sink=sink, k_dequant=k_dequant,
                     v_dequant=v_dequant, out=out, split_tokens=split_tokens, workspace=workspace,
                     kv_len=kv_len, non_causal=non_causal, q_offset=q_offset,
                     bound_min=bound_min, bound_max=bound_max,
-                    empty_rows_uniform=empty_rows_uniform, k_packed=k_packed)
+                    empty_rows_uniform=empty_rows_uniform, k_packed=k_packed,
+                    compact_kernel=compact_kernel)
 
 
 @_paged_prefill.register_fake
 def _(q, cu_seqlens_q, prior_tokens, k_cache, v_cache, block_table, out, workspace, sink,
       k_dequant, v_dequant, kv_len, bound_min, bound_max, max_seqlen_q, scale, sliding_window,
-      split_tokens, non_causal, q_offset, empty_rows_uniform, k_packed):
+      split_tokens, non_causal, q_offset, empty_rows_uniform, k_packed, compact_kernel):
     return None
 
 
@@ -338,13 +339,14 @@ def paged_prefill(q, cu_seqlens_q, prior_tokens, max_seqlen_q: int, k_cache, v_c
                   k_dequant=None, v_dequant=None, out=None, split_tokens: int = 0,
                   workspace=None, kv_len=None, non_causal: bool = False, q_offset: int = 0,
                   bound_min=None, bound_max=None, empty_rows_uniform: bool = False,
-                  k_packed: bool = False) -> Tensor:
+                  k_packed: bool = False, compact_kernel: bool = False) -> Tensor:
     if out is None:
         out = q.new_empty(q.shape, dtype=torch.bfloat16)
     _paged_prefill(q, cu_seqlens_q, prior_tokens, k_cache, v_cache, block_table, out, workspace,
                    sink, k_dequant, v_dequant, kv_len, bound_min, bound_max, int(max_seqlen_q),
                    float(scale), int(sliding_window or 0), int(split_tokens), bool(non_causal),
-                   int(q_offset), bool(empty_rows_uniform), bool(k_packed))
+                   int(q_offset), bool(empty_rows_uniform), bool(k_packed),
+                   bool(compact_kernel))
     return out
 
 
