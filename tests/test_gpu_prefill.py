@@ -302,3 +302,40 @@ def test_copy_ring_and_register_kernels_agree(gpu, fp8):
         for out in (ring, regs):
             err = (out[s0:s1].float().cpu().double() - f).abs().max().item()
             assert err <= (TOL_FP8 if fp8 else TOL_BF16), (i, err)
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_compact_kernel_matches_reference(gpu, fp8):
+    """``compact_kernel`` (the launch that fits beside a decode workgroup:
+    the 4-wave copy ring for bf16, the register-staged kernel for FP8) on a
+    multi-sequence batch with a long prior (split keys) against float64 math
+    and the default launch."""
+    cfg = W.PrefillConfig("t", 3, 16, 2, 128, 32, 300, 0, 3600, fp8=fp8, seed=91)
+    b = W.make_prefill_batch(cfg, gpu)
+    kw = {}
+    if fp8:
+        K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache, quant_mode=2,
+                   k_scale=b.k_quant, v_scale=b.v_quant, scale_per_head=True)
+        kw = dict(k_dequant=b.k_dequant, v_dequant=b.v_dequant)
+    else:
+        K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache)
+    scale = cfg.head_dim ** -0.5
+    run = lambda compact: K.paged_prefill(b.q, b.cu_seqlens, b.prior, b.max_seqlen_q, b.k_cache,
+                                          b.v_cache, b.block_table, scale=scale,
+                                          compact_kernel=compact, **kw)
+    got, base = run(True).float().cpu(), run(False).float().cpu()
+    tol = TOL_FP8 if fp8 else TOL_BF16
+    assert (got - base).abs().max().item() <= tol / 2
+    cu = b.cu_seqlens.cpu().tolist()
+    kc, vc = b.k_cache.cpu().float(), b.v_cache.cpu().float()
+    kd = b.k_dequant.cpu() if fp8 else torch.ones(cfg.kv_heads)
+    vd = b.v_dequant.cpu() if fp8 else torch.ones(cfg.kv_heads)
+    for i in range(len(cu) - 1):
+        prior = int(b.prior[i])
+        n = prior + cu[i + 1] - cu[i]
+        row = b.block_table[i].cpu()
+        ks = _seq_kv(kc, row, n, cfg.kv_heads) * kd.view(-1, 1, 1)
+        vs = _seq_kv(vc, row, n, cfg.kv_heads) * vd.view(-1, 1, 1)
+        f = OSg.fp32_prefill(b.q[cu[i]:cu[i + 1]].cpu(), ks, vs, prior, scale)
+        err = (got[cu[i]:cu[i + 1]].double() - f).abs().max().item()
+        assert err <= tol, (i, err)

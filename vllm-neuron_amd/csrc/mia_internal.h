@@ -54,6 +54,7 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &p,
 // Paged prefill: split-K plan shared by the workspace query and the launch.
 struct PrefillPlan {
   bool dma;          // bf16 / head_dim 128 kernel with the LDS copy ring
+  int dma_waves;     // its waves per workgroup (8, or 4 for compact launches)
   int rows_wg;       // query rows per workgroup
   int rows_max;      // max_seqlen_q * G
   int nsplit;        // key chunks per row tile at most (1: no split)

@@ -1310,14 +1310,19 @@ bool use_dma_kernel(const mia_prefill_args &a) {
 
 PrefillPlan plan_prefill(const mia_prefill_args &a) {
   PrefillPlan pl;
-  pl.dma = !a.compact_kernel && use_dma_kernel(a);
-  pl.rows_wg = pl.dma ? kDmaRows : kRowsWG;
+  // compact: workgroups that fit on a CU beside a decode workgroup (the
+  // copy ring with 4 waves and 2 stages, 72 KiB of LDS; FP8 caches and
+  // shapes the ring does not take use the register-staged kernel)
+  pl.dma_waves = a.compact_kernel ? 4 : kDmaWaves;
+  pl.dma = use_dma_kernel(a) && (!a.compact_kernel || (a.cache_dtype == MIA_DTYPE_BF16 &&
+                                                       a.blocks_per_seq <= dma_ids(4)));
+  pl.rows_wg = pl.dma ? dma_rows(pl.dma_waves) : kRowsWG;
   const int G = a.num_q_heads / a.num_kv_heads;
   pl.rows_max = a.max_seqlen_q * G;
   const int64_t s_ctx = (int64_t)a.blocks_per_seq * a.block_size;
   const int64_t base_wgs =
       (int64_t)((pl.rows_max + pl.rows_wg - 1) / pl.rows_wg) * a.num_kv_heads * a.num_seqs;
-  const int slots = device_cus() * (pl.dma ? 8 / kDmaWaves : 2);
+  const int slots = device_cus() * (pl.dma ? 8 / pl.dma_waves : 2);
   pl.slots = slots;
   int64_t ks = a.split_tokens;
   if (ks <= 0 && (a.non_causal || a.bound_min)) {
@@ -1417,7 +1422,10 @@ int launch_paged_prefill(const mia_prefill_args &a, const PrefillPlan &pl, hipSt
   kp.rank_items = a.num_seqs > 1 ? 1 : 0;
   const dim3 grid((unsigned)((pl.rows_max + pl.rows_wg - 1) / pl.rows_wg),
                   (unsigned)a.num_kv_heads, (unsigned)(pl.nsplit * a.num_seqs));
-  if (pl.dma) {
+  if (pl.dma && pl.dma_waves == 4) {
+    hipLaunchKernelGGL((prefill_dma_kernel<128, 4, 2, false, false>), grid, dim3(4 * 64), 0, s,
+                       kp);
+  } else if (pl.dma) {
     if (fp8 && a.k_packed)
       hipLaunchKernelGGL((prefill_dma_kernel<128, kDmaWaves, kDmaStages, true, true>), grid,
                          dim3(kDmaWaves * 64), 0, s, kp);

@@ -15,19 +15,21 @@ one split-K launch, sharing the same paged cache; the decode rows' K/V are
 written to the cache by the decode's merge kernel (after every decode
 workgroup has read the cache), not by a separate scatter launch.
 
-The two halves run concurrently: the decode (HBM-bound, a persistent grid
-of one workgroup per CU) on a side stream that forks from and joins the
-caller's stream, the prefill's K/V write and attention on the caller's
-stream with the register-staged prefill kernel (36 KB of LDS, 128 rows per
-workgroup), which fits on each CU beside a decode workgroup, where the
-copy-ring kernel's 144 KB does not.  At the Llama-3-8B mixed shape: 247 us
-against 262-276 us back to back (decode alone 184 us, prefill alone 81-86
-us); raising the decode waves' issue priority (s_setprio) changed nothing,
-and the CU-masked split of the GPU between the halves was slower than
-either (the decode needs every CU's memory parallelism: 525 / 299 / 203 us
-on 64 / 128 / 256 CUs).  ``overlap=False`` runs them back to back on the
-caller's stream.  Requirement of the overlap (as in vLLM): the decode rows
-and the prefill sequences own disjoint cache blocks.
+Under HIP-graph capture the two halves run concurrently: the decode
+(HBM-bound, a persistent grid of one workgroup per CU) on a side stream
+that forks from and joins the caller's stream, the prefill's K/V write and
+attention on the caller's stream with a compact prefill launch (the copy
+ring with 4 waves and 72 KiB of LDS), which fits on each CU beside a decode
+workgroup, where the 8-wave ring's 144 KiB does not.  At the Llama-3-8B
+mixed shape: 247 us against 262-276 us back to back (decode alone 184 us,
+prefill alone 78-81 us); raising the decode waves' issue priority
+(s_setprio) changed nothing, and the CU-masked split of the GPU between the
+halves was slower than either (the decode needs every CU's memory
+parallelism: 525 / 299 / 203 us on 64 / 128 / 256 CUs).  Issued eagerly,
+the cross-stream waits cost more than the overlap gains (389 against 263
+us), so eager calls run the halves back to back on the caller's stream.
+Requirement of the overlap (as in vLLM): the decode rows and the prefill
+sequences own disjoint cache blocks.
 """
 from __future__ import annotations
 
@@ -71,9 +73,13 @@ def mixed_batch_attention(
     v_dequant_scale: Optional[Tensor] = None,
     decode_workspace: Optional[Tensor] = None,
     prefill_workspace: Optional[Tensor] = None,
-    overlap: bool = True,
+    overlap: Optional[bool] = None,
 ) -> Tuple[Optional[Tensor], Optional[Tensor]]:
-    """Returns ``(out_decode [Bd, S_tkg, Hq, d], out_prefill [Tp, Hq, d])``."""
+    """Returns ``(out_decode [Bd, S_tkg, Hq, d], out_prefill [Tp, Hq, d])``.
+    ``overlap``: run the halves on two streams (None: when the call is being
+    captured into a HIP graph, where the fork and join are graph edges;
+    issued eagerly, the cross-stream waits cost more than the overlap
+    saves)."""
     d = V_cache.shape[-1]
     scale = softmax_scale if softmax_scale is not None else d ** -0.5
     kv_heads = V_cache.shape[1] if V_cache.dim() == 4 else 1
@@ -84,6 +90,8 @@ def mixed_batch_attention(
                    v_scale=v_scale if v_scale is not None else k_scale,
                    scale_per_head=_scale_per_head(k_scale, kv_heads))
 
+    if overlap is None:
+        overlap = torch.cuda.is_available() and torch.cuda.is_current_stream_capturing()
     both = overlap and q_prefill is not None and q_decode is not None
     out_d = None
     side = None
