@@ -339,3 +339,26 @@ def test_compact_kernel_matches_reference(gpu, fp8):
         f = OSg.fp32_prefill(b.q[cu[i]:cu[i + 1]].cpu(), ks, vs, prior, scale)
         err = (got[cu[i]:cu[i + 1]].double() - f).abs().max().item()
         assert err <= tol, (i, err)
+
+
+@pytest.mark.parametrize("split", [0, 1024])
+def test_copy_ring_output_only_8_byte_aligned(gpu, split):
+    """The copy ring stores its output rows 16 bytes per lane; an output view
+    that is only 8-byte aligned (head stride 132 elements, 4-element offset)
+    takes its 8-byte store path and holds the same values as a contiguous
+    output, for unsplit rows and for rows merged from split partials."""
+    cfg = W.PrefillConfig("t", 2, 8, 2, 128, 32, 200, 0, 2500, seed=93)
+    b = W.make_prefill_batch(cfg, gpu)
+    K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache)
+    T = b.q.shape[0]
+    wide = torch.full((T, cfg.q_heads, 136), 7.0, dtype=torch.bfloat16, device=gpu)
+    view = wide[:, :, 4:132]
+    assert view.data_ptr() % 16 == 8 and view.stride(1) == 136
+    run = lambda out: K.paged_prefill(b.q, b.cu_seqlens, b.prior, b.max_seqlen_q, b.k_cache,
+                                      b.v_cache, b.block_table, scale=cfg.head_dim ** -0.5,
+                                      split_tokens=split, out=out)
+    base = run(None)
+    run(view)
+    torch.cuda.synchronize()
+    assert torch.equal(view, base)
+    assert (wide[:, :, :4] == 7.0).all() and (wide[:, :, 132:] == 7.0).all()

@@ -1192,8 +1192,70 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
     }
   }
 
-  finish_rows<D>(p, acc_o, rm.final_max(), l_run, row_ok, seq, h, hq, (int64_t)q_begin + pos_r,
-                 r, half, kr.n_sp, sp, (p.v_deq ? p.v_deq[h] : 1.0f) * (FP8 ? 256.0f : 1.0f));
+  // ---- epilogue through LDS: the ring is free once every wave has left
+  // the loop; each wave writes its 32 rows as bf16 into its own 8 KiB
+  // (16-byte chunks XOR-swizzled by row), then stores them row-major, 16
+  // lanes per 256-byte row, so every store instruction writes 4 whole rows
+  // (the MFMA layout would write 16 bytes of each of 32 rows at a time)
+  const float vscale = (p.v_deq ? p.v_deq[h] : 1.0f) * (FP8 ? 256.0f : 1.0f);
+  const float m_fin = rm.final_max();
+  l_run += __shfl_xor(l_run, 32, 64);
+  const bool split = kr.n_sp > 1;
+  float rscale = vscale;  // split partial: o * vscale
+  if (!split) {
+    float oscale = 1.0f, denom = l_run;
+    if (p.sink) {
+      const float sink2 = p.sink[row_ok ? hq : 0] * kLog2e;
+      const float M = fmaxf(m_fin, sink2);
+      const float f = (m_fin == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m_fin - M);
+      denom = l_run * f + __builtin_amdgcn_exp2f(sink2 - M);
+      oscale = f;
+    }
+    rscale = (denom > 0.f) ? oscale * vscale / denom : 0.f;
+  }
+  __syncthreads();
+  lds_u8_t *const ob = kv_base + wave * (kRowsW * ROWB);
+#pragma unroll
+  for (int db = 0; db < DBLK; ++db)
+#pragma unroll
+    for (int e4 = 0; e4 < 4; ++e4) {
+      const int c = db * 4 + e4;  // 16-byte chunk of the row; half picks its 8 bytes
+      *(__attribute__((address_space(3))) u32x2_t *)(ob + rl * ROWB + ((c ^ (rl & 15)) << 4) +
+                                                     half * 8) =
+          u32x2_t{pack2_bf16(acc_o[db][e4 * 4] * rscale, acc_o[db][e4 * 4 + 1] * rscale),
+                  pack2_bf16(acc_o[db][e4 * 4 + 2] * rscale, acc_o[db][e4 * 4 + 3] * rscale)};
+    }
+  if (split && row_ok && half == 0) {  // the partial's m and l (fp32) after its bf16 o
+    uint8_t *w = p.ws + ((((int64_t)seq * p.Hkv + h) * p.rows_max + r) * p.nsplit + sp) *
+                            (int64_t)part_bytes(D);
+    *reinterpret_cast<float2 *>(w + 2 * D) = make_float2(m_fin, l_run);
+  }
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");  // this wave's rows are in LDS
+  constexpr int CH = ROWB / 16;  // 16-byte chunks per row
+  const bool out16 = (((uintptr_t)p.out | (uint32_t)(p.os_t | p.os_h) * 2u) & 15u) == 0;
+#pragma unroll
+  for (int i = 0; i < kRowsW * CH / 64; ++i) {
+    const int rl2 = i * (64 / CH) + lane / CH, ch = lane % CH;
+    const u32x4_t v = *(const __attribute__((address_space(3))) u32x4_t *)(
+        ob + rl2 * ROWB + ((ch ^ (rl2 & 15)) << 4));
+    const int r2 = row0 + wave * kRowsW + rl2;
+    const int pos2 = r2 / G;
+    if (r2 >= rows_total || q_begin + pos2 >= p.num_tokens) continue;
+    if (split) {
+      uint8_t *w = p.ws + ((((int64_t)seq * p.Hkv + h) * p.rows_max + r2) * p.nsplit + sp) *
+                              (int64_t)part_bytes(D);
+      *reinterpret_cast<u32x4_t *>(w + ch * 16) = v;
+    } else {
+      uint16_t *op = p.out + (int64_t)(q_begin + pos2) * p.os_t +
+                     (int64_t)(h * G + (r2 - pos2 * G)) * p.os_h + ch * 8;
+      if (out16) {
+        *reinterpret_cast<u32x4_t *>(op) = v;
+      } else {  // the output is only 8-byte aligned
+        *reinterpret_cast<u32x2_t *>(op) = u32x2_t{v[0], v[1]};
+        *reinterpret_cast<u32x2_t *>(op + 4) = u32x2_t{v[2], v[3]};
+      }
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
