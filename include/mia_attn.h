@@ -360,10 +360,11 @@ typedef struct {
   int32_t non_causal;
   int32_t q_offset;
   int32_t empty_rows_uniform;
-  /* 0: the kernel is chosen from the shapes; 1: always the register-staged
-   * kernel (128 rows and 36 KB of LDS per workgroup), which fits on a CU
+  /* 0: the kernel is chosen from the shapes; 1: a launch that fits on a CU
    * beside a decode workgroup, for a prefill that runs concurrently with a
-   * decode (a mixed batch). */
+   * decode (a mixed batch): the copy-ring kernel with 4 waves, 128 rows and
+   * 72 KiB of LDS per workgroup for bf16 caches, else the register-staged
+   * kernel (128 rows, 36 KiB). */
   int32_t compact_kernel;
 } mia_prefill_args;
 

@@ -22,17 +22,21 @@
 //        16 columns]; D/32 k-steps.  Result lane l holds tokens
 //        4*(l/16)+i, column l%16.
 //   softmax: masked scores, tile max via xor-shuffles over 16/32 lanes,
-//        online rescale (exp2 domain), per-lane partial row sums.
-//   PV : on the vector ALU in fp32: lane = (token lane, 8-wide d slice),
-//        V rows loaded 16 B per lane, probabilities exchanged through LDS.
+//        online rescale (exp2 domain, lazy: the running max only moves when
+//        a tile's max exceeds it by more than 8), per-lane partial row sums.
+//   PV : O^T = V^T P^T on v_mfma_f32_16x16x32_bf16 per 16-wide d block.  The
+//        V tile is staged in a row-swizzled LDS buffer of the wave and the
+//        V^T operand read with ds_read_b64_tr_b16; P^T comes straight from
+//        the QK accumulator registers (the k order of lane group g is tokens
+//        4g..4g+3, 16+4g..16+4g+3, so a lane's 8 probabilities are its own).
 //   The next tile's K (V) loads are issued right after QK (PV) consumed the
-//   registers, across item boundaries, so one tile of loads is always in
-//   flight; every load address is clamped into the item's attended range so
-//   no load is predicated (out-of-range rows are masked after the load).
-//   Physical block ids of an item are held one per lane and read with
-//   v_readlane (block_size % 16 == 0 keeps a 16-token group in one block).
-// End of item: xor-reduce partial sums and write (m, l, o[D]) per column to
-// the workspace.
+//   registers, across piece boundaries, so one tile of loads is always in
+//   flight; every load reads a row of an attended block (group starts are
+//   clamped into the piece, rows outside it are masked after the load), so
+//   no load is predicated.  Block-table entries are read with scalar loads
+//   (block_size % 16 == 0 keeps a 16-token group in one block).
+// End of piece: xor-reduce partial sums and write (m, l, o[D]) per column
+// to the workspace.
 //
 // Combine kernel (one wave per (column, kv head, row)): merges the row's
 // split partials, adds the S_tkg active (new) keys — which the reference
@@ -42,6 +46,13 @@
 // slots given it also performs the cache update of the active rows
 // (attention_decode.py:1081-1150) after every split kernel has read the
 // cache.
+//
+// One-pass kernel (short tables): the split kernel's tile code with one
+// eight-wave workgroup per (row, kv head) segment; the waves merge their
+// (m, l, o) through LDS, then add the active keys and the sink and store
+// bf16, with no workspace and no combine launch.  For write slots that the
+// caller declares private (each row writes slots no other row of the call
+// reads) the last wave also writes the row's active K/V into the cache.
 #include <algorithm>
 #include <mutex>
 #include <type_traits>
@@ -59,12 +70,11 @@ namespace mia {
 namespace {
 
 constexpr int kWaves = 4;
-// waves of a one-pass workgroup (one segment), two per SIMD (twelve at d =
-// 64 measured equal or slower: the per-wave chain of round trips, not the
-// tiles per wave, sets a short table's time)
-// waves of a one-pass workgroup (12 or 16 for the 17-32 tiles of the
-// Llama-3.2-1B decode, so that each streams fewer tiles one after another:
-// 13.9 -> 14.7 / 16.2 us, slower)
+// waves of a one-pass workgroup (one segment), two per SIMD (12 or 16 for
+// the 17-32 tiles of the Llama-3.2-1B decode, so that each wave streams
+// fewer tiles one after another, measured slower: 13.9 -> 14.7 / 16.2 us;
+// the per-wave chain of round trips, not the tiles per wave, sets a short
+// table's time)
 constexpr int one_waves(int) { return 8; }
 // occupancy the split kernel is compiled for: 2 workgroups per CU (8 waves,
 // 256 VGPRs each).  With streaming V loads an FP8 cache no longer needs a
