@@ -203,7 +203,11 @@ def _graph_us(fn, dev, reps: int, per_graph: int = 8, settle_s: float = 0.0) -> 
     return e0.elapsed_time(e1) * 1e3 / (reps * per_graph)
 
 
-def bench_secondary(dev, reps: int, cpu_rows: int = 0) -> dict:
+SECONDARY = ("gptoss_decode_full_b32", "gptoss_decode_swa_b32", "fp8_decode_b16_32k",
+             "llama3_1b_decode_b4", "fp8_prefill_2048", "llama3_8b_mixed_4x512_plus_60_decode")
+
+
+def bench_secondary(dev, reps: int, cpu_rows: int = 0, only=None) -> dict:
     """The other benchmark workloads, each as µs per call (HIP graph replay)
     with its algorithmic rate and roofline fraction: GPT-OSS-120B-shaped
     decode (full-attention and 128-token sliding-window layers, sinks), the
@@ -211,7 +215,8 @@ def bench_secondary(dev, reps: int, cpu_rows: int = 0) -> dict:
     prefill chunk, and the Llama-3-8B mixed batch (4 x 512 chunked prefill +
     60 decode rows) as one call against max(bytes / HBM peak, FLOPs / bf16
     peak).  With ``cpu_rows`` each entry also carries the CPU time of the
-    restated reference path for the same call (decode rows sampled)."""
+    restated reference path for the same call (decode rows sampled).
+    ``only``: names of the workloads to run (all when None)."""
     import torch
 
     from vllm_neuron_amd import _kernels as K
@@ -221,8 +226,9 @@ def bench_secondary(dev, reps: int, cpu_rows: int = 0) -> dict:
     from vllm_neuron_amd.functional.attention.attention_decode import paged_decode_core
 
     out = {}
-    for name in ("gptoss_decode_full_b32", "gptoss_decode_swa_b32", "fp8_decode_b16_32k",
-                 "llama3_1b_decode_b4"):
+    for name in SECONDARY[:4]:
+        if only is not None and name not in only:
+            continue
         cfg = W.DECODE_CONFIGS[name]
         b = W.make_decode_batch(cfg, dev)
         S_ctx = b.block_table.shape[1] * cfg.block_size
@@ -252,7 +258,9 @@ def bench_secondary(dev, reps: int, cpu_rows: int = 0) -> dict:
             rec.update(_cpu_secondary(name, b, cpu_rows))
         out[name] = rec
         del b, ws
-    for name in ("fp8_prefill_2048",):
+    for name in SECONDARY[4:5]:
+        if only is not None and name not in only:
+            continue
         cfg = W.PREFILL_CONFIGS[name]
         b = W.make_prefill_batch(cfg, dev)
         K.kv_write(b.k_new, b.v_new, b.slots, b.k_cache, b.v_cache, quant_mode=N.QUANT_MUL_F32,
@@ -273,6 +281,8 @@ def bench_secondary(dev, reps: int, cpu_rows: int = 0) -> dict:
         if cpu_rows:
             out[name].update(_cpu_secondary(name, b, cpu_rows))
         del b
+    if only is not None and SECONDARY[5] not in only:
+        return out
     m = W.make_mixed_batch(dev)
     db, pb = m.decode, m.prefill
     dws = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
@@ -581,6 +591,9 @@ def main() -> int:
                          "times (the reference kernel for scaling HBM byte counters)")
     ap.add_argument("--only", choices=("decode", "prefill"), default=None,
                     help="run one leg only (for profiler runs) and print its timing as JSON")
+    ap.add_argument("--secondary", choices=SECONDARY, action="append", default=None,
+                    help="run only these secondary workloads (repeatable; for profiler runs) "
+                         "and print their JSON")
     ap.add_argument("--no-secondary", action="store_true",
                     help="skip the other workloads (GPT-OSS decode, FP8 decode and chunk, "
                          "Llama-3.2-1B decode, mixed batch)")
@@ -610,6 +623,10 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.secondary:
+        sec = bench_secondary(dev, max(4, args.steps // 8), 0, only=set(args.secondary))
+        print(json.dumps({"secondary": sec}), flush=True)
+        return 0
     if args.only == "prefill":
         pre = bench_prefill(dev, max(5, args.steps // 2), max(2, args.warmup // 2))
         print(json.dumps({"workload": "llama3_8b_chunked_prefill_4x512_prior0-4096",
