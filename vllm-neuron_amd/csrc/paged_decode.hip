@@ -965,8 +965,9 @@ MIA_DEV void split_body(const P &c) {
       const int64_t kb0 = cur.b * c.kn_b + (int64_t)cur.h * c.kn_h;
       const int64_t vb0 = cur.b * c.vn_b + (int64_t)cur.h * c.vn_h;
       uint16_t k0[KSTEPS][8], v0[DB16][4];
-      float sink_v = 0.f;
+      float sink_v = 0.f, vdeq = 1.0f;
       if (wave == 0) {
+        if (c.v_deq) vdeq = c.v_deq[cur.h];
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks)
 #pragma unroll
@@ -1022,10 +1023,9 @@ MIA_DEV void split_body(const P &c) {
         m = m_new;
       };
       const float ascale = c.act_scale_log2 * kdq_cur;
-#pragma nounroll
-      for (int k = 0; k < p.S; ++k) {
-        const int64_t kb = cur.b * c.kn_b + (int64_t)k * c.kn_s + (int64_t)cur.h * c.kn_h;
-        const int64_t vb = cur.b * c.vn_b + (int64_t)k * c.vn_s + (int64_t)cur.h * c.vn_h;
+      // active token k with its K and V rows as floats (after the cache's
+      // quantise round trip)
+      auto active_token = [&](int k, const float (&kf)[KSTEPS][8], const float (&vf)[DB16][4]) {
         float dot = 0.f;
 #pragma unroll
         for (int ks = 0; ks < KSTEPS; ++ks) {
@@ -1033,10 +1033,7 @@ MIA_DEV void split_body(const P &c) {
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
             const float qv = __uint_as_float((e & 1) ? (qw[e >> 1] & 0xffff0000u) : (qw[e >> 1] << 16));
-            const float kv = quant_roundtrip(
-                c, bf16_bits_to_f32(k == 0 ? k0[ks][e] : c.k_new[kb + kd0(ks, kg) + e]), cur.h,
-                c.k_quant);
-            dot = fmaf(qv, kv, dot);
+            dot = fmaf(qv, kf[ks][e], dot);
           }
         }
         dot = wave_sum_xor(dot, 16);
@@ -1050,28 +1047,80 @@ MIA_DEV void split_body(const P &c) {
         } else {
           ok = k <= s_q;
         }
-        float vv[DB16][4];
+        absorb(ok ? dot * ascale : -INFINITY, vf, true);
+      };
+      // token 0 from the rows loaded before the barrier.  The quantise mode
+      // is tested once here, not per element inside the unrolled products,
+      // so the common path (no round trip) is short straight-line code: the
+      // general form, with the round trip inlined for every element, made
+      // this tail ~5k instructions that the wave fetched past.
+      if (p.S > 0) {
+        float kf[KSTEPS][8], vf[DB16][4];
+        if (c.quant_mode == MIA_QUANT_NONE) {
+#pragma unroll
+          for (int ks = 0; ks < KSTEPS; ++ks)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) kf[ks][e] = bf16_bits_to_f32(k0[ks][e]);
+#pragma unroll
+          for (int blk = 0; blk < DB16; ++blk)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) vf[blk][i] = bf16_bits_to_f32(v0[blk][i]);
+        } else {
+#pragma unroll
+          for (int ks = 0; ks < KSTEPS; ++ks)
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              kf[ks][e] = quant_roundtrip(c, bf16_bits_to_f32(k0[ks][e]), cur.h, c.k_quant);
+#pragma unroll
+          for (int blk = 0; blk < DB16; ++blk)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              vf[blk][i] = quant_roundtrip(c, bf16_bits_to_f32(v0[blk][i]), cur.h, c.v_quant);
+        }
+        active_token(0, kf, vf);
+      }
+#pragma nounroll
+      for (int k = 1; k < p.S; ++k) {
+        const int64_t kb = cur.b * c.kn_b + (int64_t)k * c.kn_s + (int64_t)cur.h * c.kn_h;
+        const int64_t vb = cur.b * c.vn_b + (int64_t)k * c.vn_s + (int64_t)cur.h * c.vn_h;
+        float kf[KSTEPS][8], vf[DB16][4];
+#pragma unroll
+        for (int ks = 0; ks < KSTEPS; ++ks)
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            kf[ks][e] = quant_roundtrip(c, bf16_bits_to_f32(c.k_new[kb + kd0(ks, kg) + e]), cur.h,
+                                        c.k_quant);
 #pragma unroll
         for (int blk = 0; blk < DB16; ++blk)
 #pragma unroll
           for (int i = 0; i < 4; ++i)
-            vv[blk][i] = quant_roundtrip(
-                c, bf16_bits_to_f32(k == 0 ? v0[blk][i] : c.v_new[vb + 16 * blk + 4 * kg + i]),
-                cur.h, c.v_quant);
-        absorb(ok ? dot * ascale : -INFINITY, vv, true);
+            vf[blk][i] = quant_roundtrip(c, bf16_bits_to_f32(c.v_new[vb + 16 * blk + 4 * kg + i]),
+                                         cur.h, c.v_quant);
+        active_token(k, kf, vf);
       }
       if (c.sink) {  // the sink logit joins the denominator only
         const float vz[DB16][4] = {};
         absorb(sink_v * kLog2e, vz, false);
       }
       if (col_ok) {
-        const float vdeq = c.v_deq ? c.v_deq[cur.h] : 1.0f;
         uint16_t *op = c.out + cur.b * c.os_b + (int64_t)s_q * c.os_s + hq * c.os_h;
+        // 4 consecutive d of the column per lane and block: one 8-byte store
+        // when the output allows it
+        const bool st8 = (((uintptr_t)c.out | (uint64_t)(c.os_b | c.os_s | c.os_h) * 2u) & 7u) == 0;
 #pragma unroll
-        for (int blk = 0; blk < DB16; ++blk)
+        for (int blk = 0; blk < DB16; ++blk) {
+          uint16_t o4[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            op[16 * blk + 4 * kg + i] = (uint16_t)f32_to_bf16_bits(oacc[blk][i] / l * vdeq);
+          for (int i = 0; i < 4; ++i) o4[i] = (uint16_t)f32_to_bf16_bits(oacc[blk][i] / l * vdeq);
+          uint16_t *dst = op + 16 * blk + 4 * kg;
+          if (st8) {
+            *reinterpret_cast<u32x2_t *>(dst) =
+                u32x2_t{o4[0] | ((uint32_t)o4[1] << 16), o4[2] | ((uint32_t)o4[3] << 16)};
+          } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) dst[i] = o4[i];
+          }
+        }
       }
       break;
     }
