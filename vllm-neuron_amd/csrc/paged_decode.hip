@@ -1039,10 +1039,10 @@ MIA_DEV void split_body(const P &c) {
         dot = wave_sum_xor(dot, 16);
         dot = wave_sum_xor(dot, 32);
         bool ok;
-        if (p.mask_mode == 1) {
+        if (__builtin_expect(p.mask_mode == 1, 0)) {
           const int64_t lin = seq_to_linear((int64_t)p.s_ctx - p.S + k, p.mask_bl);
           ok = p.full_mask[((lin * p.B + cur.b) * p.Hq + hq) * p.S + s_q] != 0.f;
-        } else if (c.active_mask) {
+        } else if (__builtin_expect(c.active_mask != nullptr, 0)) {
           ok = c.active_mask[(((int64_t)k * p.B + cur.b) * p.Hq + hq) * p.S + s_q] != 0.f;
         } else {
           ok = k <= s_q;
@@ -1056,7 +1056,7 @@ MIA_DEV void split_body(const P &c) {
       // this tail ~5k instructions that the wave fetched past.
       if (p.S > 0) {
         float kf[KSTEPS][8], vf[DB16][4];
-        if (c.quant_mode == MIA_QUANT_NONE) {
+        if (__builtin_expect(c.quant_mode == MIA_QUANT_NONE, 1)) {
 #pragma unroll
           for (int ks = 0; ks < KSTEPS; ++ks)
 #pragma unroll
@@ -1080,7 +1080,7 @@ MIA_DEV void split_body(const P &c) {
         active_token(0, kf, vf);
       }
 #pragma nounroll
-      for (int k = 1; k < p.S; ++k) {
+      for (int k = 1; __builtin_expect(k < p.S, 0); ++k) {
         const int64_t kb = cur.b * c.kn_b + (int64_t)k * c.kn_s + (int64_t)cur.h * c.kn_h;
         const int64_t vb = cur.b * c.vn_b + (int64_t)k * c.vn_s + (int64_t)cur.h * c.vn_h;
         float kf[KSTEPS][8], vf[DB16][4];
@@ -1107,11 +1107,12 @@ MIA_DEV void split_body(const P &c) {
         // 4 consecutive d of the column per lane and block: one 8-byte store
         // when the output allows it
         const bool st8 = (((uintptr_t)c.out | (uint64_t)(c.os_b | c.os_s | c.os_h) * 2u) & 7u) == 0;
+        const float inv = vdeq / l;  // one division instead of one per element
 #pragma unroll
         for (int blk = 0; blk < DB16; ++blk) {
           uint16_t o4[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) o4[i] = (uint16_t)f32_to_bf16_bits(oacc[blk][i] / l * vdeq);
+          for (int i = 0; i < 4; ++i) o4[i] = (uint16_t)f32_to_bf16_bits(oacc[blk][i] * inv);
           uint16_t *dst = op + 16 * blk + 4 * kg;
           if (st8) {
             *reinterpret_cast<u32x2_t *>(dst) =
