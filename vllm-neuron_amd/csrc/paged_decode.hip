@@ -835,7 +835,7 @@ MIA_DEV void split_body(const P &c) {
               sc[st][i] = ok ? sc[st][i] * scale2 : -INFINITY;
             }
         }
-      } else if (p.mask_mode == 0) {
+      } else if (__builtin_expect(p.mask_mode == 0, 1)) {  // else: a mask tensor (rare)
 #pragma unroll
         for (int st = 0; st < NSUB; ++st)
 #pragma unroll
@@ -1256,7 +1256,29 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(CombineParams c) {
 #pragma unroll
   for (int j = 0; j < DPL; ++j) acc[j] *= vpart_scale;
 
-  // ---- active keys (the last S slots of the gathered context)
+  // ---- active keys (the last S slots of the gathered context).  Their
+  // rows as floats after the cache's quantise round trip, with the quantise
+  // mode tested once (inlined per element it spread the common path over
+  // thousands of instructions); the rare paths are marked unlikely so the
+  // common one is laid out contiguously.
+  float kf[MAXS][DPL], vf[MAXS][DPL];
+  if (__builtin_expect(c.quant_mode == MIA_QUANT_NONE, 1)) {
+#pragma unroll
+    for (int k = 0; k < MAXS; ++k)
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        kf[k][j] = k < S ? bf16_bits_to_f32(kraw[k][j]) : 0.f;
+        vf[k][j] = k < S ? bf16_bits_to_f32(vraw[k][j]) : 0.f;
+      }
+  } else {
+#pragma unroll
+    for (int k = 0; k < MAXS; ++k)
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) {
+        kf[k][j] = k < S ? quant_roundtrip(c, bf16_bits_to_f32(kraw[k][j]), h, c.k_quant) : 0.f;
+        vf[k][j] = k < S ? quant_roundtrip(c, bf16_bits_to_f32(vraw[k][j]), h, c.v_quant) : 0.f;
+      }
+  }
   const float ascale = c.act_scale_log2 * kdeq;
   float sk[MAXS];
 #pragma unroll
@@ -1264,18 +1286,17 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(CombineParams c) {
     sk[k] = -INFINITY;
     if (k < S) {
       bool ok;
-      if (p.mask_mode == 1) {
+      if (__builtin_expect(p.mask_mode == 1, 0)) {
         const int64_t lin = seq_to_linear((int64_t)p.s_ctx - S + k, p.mask_bl);
         ok = p.full_mask[((lin * p.B + b) * p.Hq + hq) * S + s_q] != 0.f;
-      } else if (c.active_mask) {
+      } else if (__builtin_expect(c.active_mask != nullptr, 0)) {
         ok = c.active_mask[(((int64_t)k * p.B + b) * p.Hq + hq) * S + s_q] != 0.f;
       } else {
         ok = k <= s_q;
       }
       float dot = 0.f;
 #pragma unroll
-      for (int j = 0; j < DPL; ++j)
-        dot = fmaf(q[j], quant_roundtrip(c, bf16_bits_to_f32(kraw[k][j]), h, c.k_quant), dot);
+      for (int j = 0; j < DPL; ++j) dot = fmaf(q[j], kf[k][j], dot);
 #pragma unroll
       for (int m = 32; m >= 1; m >>= 1) dot = wave_sum_xor(dot, m);
       if (ok) sk[k] = dot * ascale;
@@ -1295,8 +1316,7 @@ __global__ __launch_bounds__(64) void decode_combine_kernel(CombineParams c) {
       const float pk = __builtin_amdgcn_exp2f(sk[k] - bmu);
       L += pk;
 #pragma unroll
-      for (int j = 0; j < DPL; ++j)
-        acc[j] += pk * quant_roundtrip(c, bf16_bits_to_f32(vraw[k][j]), h, c.v_quant);
+      for (int j = 0; j < DPL; ++j) acc[j] += pk * vf[k][j];
     }
   }
   uint16_t *op = c.out + b * c.os_b + (int64_t)s_q * c.os_s + hq * c.os_h;
