@@ -576,8 +576,11 @@ MIA_DEV void split_body(const P &c) {
   // The piece of this wave starting at flattened tile x (x < x_end): its
   // segment (b, h) by binary search over R, its tokens and partial slot.  An
   // x past the wave's range yields `fallback` with valid = 0 (so its loads
-  // stay in bounds).
-  auto decode_piece = [&](int x, const Item &fallback) {
+  // stay in bounds).  Without `slot` the partial slot is left for later, as
+  // -(segment start) - 1: locating the segment's first wave is a binary
+  // search over the weighted shares (~1 us), which the first piece runs
+  // after its first tile's loads are issued.
+  auto decode_piece = [&](int x, const Item &fallback, bool slot) {
     Item it;
     if (x >= x_end) {
       it = fallback;
@@ -601,7 +604,7 @@ MIA_DEV void split_body(const P &c) {
     it.valid = 1;
     it.b = b;
     it.h = h;
-    it.j = w_id - wave_of_tile(p, seg0, n_tiles, n_waves);
+    it.j = slot ? w_id - wave_of_tile(p, seg0, n_tiles, n_waves) : -seg0 - 1;
     it.t_lo = max(row_lo, tile0 * kTile);
     it.t_hi = min(row_hi, (tile0 + (end - x)) * kTile);
     it.next_x = end;
@@ -750,7 +753,7 @@ MIA_DEV void split_body(const P &c) {
     cur.next_x = 0;
     cur.minpos = __builtin_bit_cast(float, readfirstlane(__builtin_bit_cast(int, ri.minpos)));
   } else {
-    cur = decode_piece(x_begin, Item{});
+    cur = decode_piece(x_begin, Item{}, false);
   }
   bf16x8_t q_cur[KSTEPS];
   load_q(cur, q_cur);
@@ -770,6 +773,7 @@ MIA_DEV void split_body(const P &c) {
     issue_k(kr, cur, r0);
     issue_v(vr, cur, r0, first_tile(cur));
   }
+  if constexpr (!ONE) cur.j = w_id - wave_of_tile(p, -cur.j - 1, n_tiles, n_waves);
 
   while (true) {
     Item nxt;
@@ -777,7 +781,7 @@ MIA_DEV void split_body(const P &c) {
       nxt = cur;
       nxt.valid = 0;
     } else {
-      nxt = decode_piece(cur.next_x, cur);
+      nxt = decode_piece(cur.next_x, cur, true);
     }
     bf16x8_t q_land[KSTEPS];
     load_q(nxt, q_land);
