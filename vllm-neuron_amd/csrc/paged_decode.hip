@@ -95,8 +95,12 @@ constexpr int kPMax = 128;
 constexpr int kMaxMinTiles = 8;        // longest minimum tile range of a streaming wave
 // share weight of a streaming wave by dispatch class (see share_prefix);
 // two classes are populated at two workgroups per CU (FP8: 8 : 7 measured
-// 1 % faster than 8 : 6, 8 : 8 and 8 : 5 slower on the B=16 32k decode)
-constexpr int kClassWeightBf16[3] = {5, 4, 4};
+// 1 % faster than 8 : 6, 8 : 8 and 8 : 5 slower on the B=16 32k decode;
+// bf16 d = 64: 7 : 5 against 5 : 4, 4 : 3, 3 : 2 and 8 : 5 on the GPT-OSS
+// full layer 99.1 against 99.6, 99.5, 99.8 and 99.8 us, same box; per-wave
+// timestamps at 5 : 4 showed the first class ending at 77 us on average,
+// the second at 86 us).  A bf16 d = 128 grid has one class.
+constexpr int kClassWeightBf16[3] = {7, 5, 4};
 constexpr int kClassWeightFp8[3] = {8, 7, 4};
 constexpr int kMaxClassWeight = 8;
 constexpr int kMaxDeviceCUs = 1024;  // the weighted prefix stays below 2^22
