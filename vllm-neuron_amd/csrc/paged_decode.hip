@@ -461,6 +461,17 @@ MIA_DEV void split_body(const P &c) {
   __shared__ int s_hi[kMaxRows];
   __shared__ float s_minpos[kMaxRows];
   __shared__ float s_one_m[NW][16], s_one_l[NW][16];  // one-pass merge
+  // Partials of a streaming wave's pieces other than its last, kept in LDS
+  // until its stream ends: a vector store in the stream delays every later
+  // load wait of the wave (the memory counter completes in order), and a
+  // piece boundary with its partial stored at once cost the wave ~3 us
+  // (Llama-3-8B decode: waves with two pieces ended 3.4 us after those with
+  // one).  KDEF partials per wave within a per-wave LDS budget (0: none).
+  constexpr int PBYTES = NCP * D * 4;
+  constexpr int KDEF =
+      ONE ? 0 : std::min(2, (grid_wg_per_cu(D, FP8) == 1 ? 16384 : 4096) / PBYTES);
+  __shared__ __attribute__((aligned(16))) uint8_t def_o[KDEF > 0 ? NW : 1][KDEF > 0 ? KDEF * PBYTES : 16];
+  __shared__ float2 def_ml[KDEF > 0 ? NW : 1][KDEF > 0 ? KDEF : 1][NCP];
 
   const int wave = threadIdx.x >> 6;
   const int lane = threadIdx.x & 63;
@@ -738,6 +749,51 @@ MIA_DEV void split_body(const P &c) {
     }
     if (lane < nvalid)
       *reinterpret_cast<float2 *>(p.ws_ml + (ws_row + p.col0 + lane) * 2) = make_float2(m, l);
+  };
+  // staged partials of this wave (see def_o): slot k holds the piece with
+  // workspace row def_row[k], slot def_j[k], and the piece count to write at
+  // def_cnt[k] (-1: none)
+  int n_def = 0;
+  int64_t def_row[KDEF > 0 ? KDEF : 1] = {};
+  int def_j[KDEF > 0 ? KDEF : 1] = {};
+  int def_cnt[KDEF > 0 ? KDEF : 1] = {};
+  auto stage_partial = [&](const f32x4_t (&o)[DB16], float m, float l, int k) {
+    if constexpr (KDEF > 0) {
+      typedef __attribute__((address_space(3))) f32x4_t lds_f32x4_t;
+      lds_u8_t *const dst = (lds_u8_t *)&def_o[wave][0] + k * PBYTES;
+      if (qcol < NCP) {  // a slot holds NCP columns (lanes of columns past NCP hold padding)
+#pragma unroll
+        for (int blk = 0; blk < DB16; ++blk)  // [column][d], as write_partial stages it
+          *(lds_f32x4_t *)(dst + (qcol * D + 16 * blk + 4 * kg) * 4) = o[blk];
+      }
+      if (lane < NCP) def_ml[wave][k][lane] = make_float2(m, l);
+    } else {
+      (void)o, (void)m, (void)l, (void)k;
+    }
+  };
+  auto flush_partials = [&]() {
+    if constexpr (KDEF > 0) {
+      typedef __attribute__((address_space(3))) f32x4_t lds_f32x4_t;
+      const int nvalid = min(NCP, p.nc_tot - p.col0);  // columns with workspace rows
+      constexpr int kStores = NCP * D * 4 / 1024;       // 16 bytes per lane each
+#pragma unroll
+      for (int k = 0; k < KDEF; ++k) {
+        if (k >= n_def) break;
+        if (def_j[k] >= p.num_splits) continue;  // never: at most num_splits pieces
+        const lds_u8_t *src = (const lds_u8_t *)&def_o[wave][0] + k * PBYTES;
+        float *const dst = p.ws_o + (def_row[k] + p.col0) * D;
+#pragma unroll
+        for (int st = 0; st < kStores; ++st) {
+          const int e = st * 256 + lane * 4;
+          if (e / D < nvalid)
+            *reinterpret_cast<f32x4_t *>(dst + e) = *(const lds_f32x4_t *)(src + e * 4);
+        }
+        if (lane < nvalid)
+          *reinterpret_cast<float2 *>(p.ws_ml + (def_row[k] + p.col0 + lane) * 2) =
+              def_ml[wave][k][lane];
+        if (def_cnt[k] >= 0 && lane == 0) p.ws_cnt[def_cnt[k]] = def_j[k] + 1;
+      }
+    }
   };
   Item cur;
   if constexpr (ONE) {
@@ -1134,14 +1190,30 @@ MIA_DEV void split_body(const P &c) {
       break;
     }
     const int64_t ws_row = (((int64_t)cur.b * p.Hkv + cur.h) * p.num_splits + cur.j) * p.nc_tot;
-    write_partial(oacc, m_run, l_run, ws_row, cur.j);
     // the segment's piece count, for the combine, from the piece that ends
     // at the row's attended end (read from LDS here rather than carried in
     // the piece registers; each column-group launch writes the same value)
-    if (cur.t_hi >= readfirstlane(s_hi[cur.b]) && lane == 0)
-      p.ws_cnt[cur.b * p.Hkv + cur.h] = cur.j + 1;
+    const bool cnt_here = cur.t_hi >= readfirstlane(s_hi[cur.b]);
+    const int cnt_at = cur.b * p.Hkv + cur.h;
+    if (nxt.valid && n_def < KDEF) {  // not the last piece: stage it in LDS
+      stage_partial(oacc, m_run, l_run, n_def);
+#pragma unroll
+      for (int k = 0; k < (KDEF > 0 ? KDEF : 1); ++k)
+        if (k == n_def) {
+          def_row[k] = ws_row;
+          def_j[k] = cur.j;
+          def_cnt[k] = cnt_here ? cnt_at : -1;
+        }
+      ++n_def;
+    } else {
+      write_partial(oacc, m_run, l_run, ws_row, cur.j);
+      if (cnt_here && lane == 0) p.ws_cnt[cnt_at] = cur.j + 1;
+    }
 
-    if (!nxt.valid) break;
+    if (!nxt.valid) {
+      flush_partials();
+      break;
+    }
     cur = nxt;
 #pragma unroll
     for (int ks = 0; ks < KSTEPS; ++ks) q_cur[ks] = q_hold[ks];
