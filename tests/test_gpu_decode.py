@@ -515,3 +515,26 @@ def test_head_dims_other_than_64_and_128(gpu, d, extra):
         torch.cuda.synchronize()
         assert torch.equal(b.k_cache.view(torch.uint8), kc.view(torch.uint8))
         assert torch.equal(b.v_cache.view(torch.uint8), vc.view(torch.uint8))
+
+
+@pytest.mark.parametrize("kw", [
+    dict(q_heads=32, kv_heads=8, head_dim=128, block_size=32),            # bf16 d=128, 4 columns
+    dict(q_heads=16, kv_heads=2, head_dim=64, block_size=16, sink=True),  # bf16 d=64, 8 columns
+    dict(q_heads=48, kv_heads=8, head_dim=128, block_size=64, fp8=True),  # FP8, 6 columns
+    dict(q_heads=128, kv_heads=8, head_dim=128, block_size=32),           # 16 columns
+])
+def test_many_pieces_per_wave(gpu, kw):
+    """Short rows with long streaming shares: every wave's share spans many
+    (row, kv head) segments, so each wave ends many pieces.  The partials of
+    its first pieces are staged in LDS and stored when its stream ends, the
+    ones past the staging capacity are stored at once.  Against float64 math,
+    and within tolerance of the same call with one-tile shares."""
+    cfg = _small_cfg(batch=48, ctx_lo=33, ctx_hi=200, seed=123, **kw)
+    b = _make(cfg, gpu)
+    ref = _fp32(b, cfg.head_dim ** -0.5)
+    tol = TOL_FP8 if cfg.fp8 else TOL_BF16
+    many = _run_core(b, split_tokens=4096).float().cpu()
+    few = _run_core(b, split_tokens=32).float().cpu()
+    assert torch.isfinite(many).all()
+    assert (many.double() - ref).abs().max().item() <= tol
+    assert (few.double() - ref).abs().max().item() <= tol
