@@ -1497,11 +1497,13 @@ int decode_noalloc_scratch(void **ptr) {
 }
 
 // one-pass kernel: tables of at most kOnePassTiles tiles (GPT-OSS 128-token
-// window: 13.6 against 21.7 us), or of at most kOnePassTilesFew when every
-// segment's workgroup fits on the device at once and no cache write follows
-// (Llama-3.2-1B, B=4, 1024 tokens: 16.5 against 17.7 us without a write;
-// with one the split path's combine writes the rows for free, 18.1 against
-// 18.5 us with the scatter launch after the one-pass kernel)
+// window: 13.6 against 21.7 us with the scatter launch after it), or of at
+// most kOnePassTilesFew when every segment's workgroup fits on the device at
+// once and no scatter launch follows: no cache write, or private write slots
+// that the kernel writes itself (Llama-3.2-1B, B=4, 1024 tokens: 16.5
+// against 17.7 us without a write; with a shared-slot write the split
+// path's combine writes the rows for free, 18.1 against 18.5 us with the
+// scatter launch)
 constexpr int kOnePassTiles = 8;
 constexpr int kOnePassTilesFew = 32;
 
@@ -1534,11 +1536,12 @@ DecodePlan plan_decode(const mia_decode_args &a) {
   const int64_t wg = (std::max<int64_t>(1, n_max / mt) + kWaves - 1) / kWaves;
   const int64_t cap = wgs_cu * (int64_t)device_cu_count();
   pl.grid = (int)std::max<int64_t>(1, std::min(wg, cap));
-  // Short tables (sliding-window layers, short contexts): one wave streams
-  // a whole (row, kv head) segment and writes the output itself, saving the
-  // shares, the partials and the combine launch.  A given write_slots is
-  // then served by the cache-write kernel after the attention, which needs
-  // the active rows of the batch as one token sequence.
+  // Short tables (sliding-window layers, short contexts): one workgroup
+  // takes a whole (row, kv head) segment and writes the output itself,
+  // saving the shares, the partials and the combine launch.  A given
+  // write_slots that is not private is then served by the cache-write
+  // kernel after the attention, which needs the active rows of the batch as
+  // one token sequence.
   const bool flat_new =
       a.batch <= 1 || (a.k_new_stride[0] == (int64_t)a.s_active * a.k_new_stride[1] &&
                        a.v_new_stride[0] == (int64_t)a.s_active * a.v_new_stride[1]);
