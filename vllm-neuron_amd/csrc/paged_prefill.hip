@@ -313,24 +313,35 @@ MIA_DEV uint3 ranked_tile(const PrefillKParams &p, int *scratch, int cap, SeqInf
   const uint32_t lane = tid & 63, nw = NT >> 6;
   const uint32_t wv = (uint32_t)readfirstlane((int)(tid >> 6));
   const uint32_t nch = (n_x + 63) / 64;  // uniform
-  int cm[kChunks];
-#pragma unroll
-  for (uint32_t u = 0; u < kChunks; ++u)
-    cm[u] = (u < nch && 64 * u + lane < n_x) ? scratch[64 * u + lane] : -1;
   // lane m holds the cost of the wave's m-th item (at most 64: n_x <= NT)
   const int c_mine = wv + nw * lane < n_x ? scratch[wv + nw * lane] : 0;
   const uint32_t n_mine = (n_x + nw - 1 - wv) / nw;
   int found = -1;
-  for (uint32_t m = 0; m < n_mine; ++m) {
-    const uint32_t j = wv + nw * m;
-    const int cj = __builtin_amdgcn_readlane(c_mine, (int)m);
-    uint32_t rank = 0;
+  if (nch == 1) {  // at most 64 items: one ballot per ranked item
+    const int c0 = lane < n_x ? scratch[lane] : -1;
+    for (uint32_t m = 0; m < n_mine; ++m) {
+      const uint32_t j = wv + nw * m;
+      const int cj = __builtin_amdgcn_readlane(c_mine, (int)m);
+      const uint32_t rank = (uint32_t)__builtin_popcountll(
+          __builtin_amdgcn_ballot_w64(c0 > cj || (c0 == cj && lane < j)));
+      if (rank == k) found = (int)j;
+    }
+  } else {
+    int cm[kChunks];
 #pragma unroll
     for (uint32_t u = 0; u < kChunks; ++u)
-      if (u < nch)
-        rank += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(
-            cm[u] > cj || (cm[u] == cj && 64 * u + lane < j)));
-    if (rank == k) found = (int)j;
+      cm[u] = (u < nch && 64 * u + lane < n_x) ? scratch[64 * u + lane] : -1;
+    for (uint32_t m = 0; m < n_mine; ++m) {
+      const uint32_t j = wv + nw * m;
+      const int cj = __builtin_amdgcn_readlane(c_mine, (int)m);
+      uint32_t rank = 0;
+#pragma unroll
+      for (uint32_t u = 0; u < kChunks; ++u)
+        if (u < nch)
+          rank += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(
+              cm[u] > cj || (cm[u] == cj && 64 * u + lane < j)));
+      if (rank == k) found = (int)j;
+    }
   }
   if (found >= 0 && lane == 0) scratch[n_x] = found;
   __syncthreads();
