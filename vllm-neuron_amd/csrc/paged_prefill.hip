@@ -275,6 +275,32 @@ constexpr uint32_t kRankMax = 512;  // items per XCD ranked at most
 // when the host did not ask for ranking, the group count is not a multiple
 // of 8 or an XCD has more items than the scratch, NT or kRankMax.  NT is a
 // template argument: blockDim.x would be a load from the dispatch arguments.
+// The item of rank k among the n_x costs in scratch (ties keep the index
+// order): costs are held 64 per chunk in NC registers (-1 past the items:
+// costs are >= 0), and the wave ranks every nw-th item with one ballot per
+// chunk; the loop runs in scalar registers (wave-uniform bounds, v_readlane
+// for the ranked item's cost).  Returns the index, or -1 when none of the
+// wave's items has rank k.
+template <int NC>
+MIA_DEV int rank_find(const int *scratch, uint32_t n_x, uint32_t lane, uint32_t wv, uint32_t nw,
+                      uint32_t k, int c_mine, uint32_t n_mine) {
+  int cm[NC];
+#pragma unroll
+  for (int u = 0; u < NC; ++u) cm[u] = 64u * u + lane < n_x ? scratch[64 * u + lane] : -1;
+  int found = -1;
+  for (uint32_t m = 0; m < n_mine; ++m) {
+    const uint32_t j = wv + nw * m;
+    const int cj = __builtin_amdgcn_readlane(c_mine, (int)m);
+    uint32_t rank = 0;
+#pragma unroll
+    for (int u = 0; u < NC; ++u)
+      rank += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(
+          cm[u] > cj || (cm[u] == cj && 64u * u + lane < j)));
+    if (rank == k) found = (int)j;
+  }
+  return found;
+}
+
 template <uint32_t NT>
 MIA_DEV uint3 ranked_tile(const PrefillKParams &p, int *scratch, int cap, SeqInfo &info) {
   constexpr uint32_t X = 8;
@@ -302,47 +328,21 @@ MIA_DEV uint3 ranked_tile(const PrefillKParams &p, int *scratch, int cap, SeqInf
         i32x4_t{mine.q_begin, mine.S_q, mine.prior, 0};
   }
   __syncthreads();
-  // rank of item j: items of higher cost, or of equal cost and lower index,
-  // counted 64 at a time with a ballot; each wave ranks every nw-th item.
-  // The costs are read from LDS once (lane i holds items i, i + 64, ...,
-  // -1 past the items: costs are >= 0, and lane m the cost of the wave's
-  // m-th item) and the loop runs in scalar registers (wave-uniform bounds,
-  // v_readlane for the ranked item's cost); the chosen index is stored
-  // once, after the loop.
-  constexpr uint32_t kChunks = (kRankMax < NT ? kRankMax : NT) / 64;
+  // rank of item j: items of higher cost, or of equal cost and lower index;
+  // each wave ranks every nw-th item (rank_find) and the chosen index is
+  // stored once, after the loop.
   const uint32_t lane = tid & 63, nw = NT >> 6;
   const uint32_t wv = (uint32_t)readfirstlane((int)(tid >> 6));
   const uint32_t nch = (n_x + 63) / 64;  // uniform
   // lane m holds the cost of the wave's m-th item (at most 64: n_x <= NT)
   const int c_mine = wv + nw * lane < n_x ? scratch[wv + nw * lane] : 0;
   const uint32_t n_mine = (n_x + nw - 1 - wv) / nw;
-  int found = -1;
-  if (nch == 1) {  // at most 64 items: one ballot per ranked item
-    const int c0 = lane < n_x ? scratch[lane] : -1;
-    for (uint32_t m = 0; m < n_mine; ++m) {
-      const uint32_t j = wv + nw * m;
-      const int cj = __builtin_amdgcn_readlane(c_mine, (int)m);
-      const uint32_t rank = (uint32_t)__builtin_popcountll(
-          __builtin_amdgcn_ballot_w64(c0 > cj || (c0 == cj && lane < j)));
-      if (rank == k) found = (int)j;
-    }
-  } else {
-    int cm[kChunks];
-#pragma unroll
-    for (uint32_t u = 0; u < kChunks; ++u)
-      cm[u] = (u < nch && 64 * u + lane < n_x) ? scratch[64 * u + lane] : -1;
-    for (uint32_t m = 0; m < n_mine; ++m) {
-      const uint32_t j = wv + nw * m;
-      const int cj = __builtin_amdgcn_readlane(c_mine, (int)m);
-      uint32_t rank = 0;
-#pragma unroll
-      for (uint32_t u = 0; u < kChunks; ++u)
-        if (u < nch)
-          rank += (uint32_t)__builtin_popcountll(__builtin_amdgcn_ballot_w64(
-              cm[u] > cj || (cm[u] == cj && 64 * u + lane < j)));
-      if (rank == k) found = (int)j;
-    }
-  }
+  // the loop for the smallest chunk count that holds the items (n_x <= 512)
+  int found;
+  if (nch <= 1) found = rank_find<1>(scratch, n_x, lane, wv, nw, k, c_mine, n_mine);
+  else if (nch <= 2) found = rank_find<2>(scratch, n_x, lane, wv, nw, k, c_mine, n_mine);
+  else if (nch <= 4) found = rank_find<4>(scratch, n_x, lane, wv, nw, k, c_mine, n_mine);
+  else found = rank_find<8>(scratch, n_x, lane, wv, nw, k, c_mine, n_mine);
   if (found >= 0 && lane == 0) scratch[n_x] = found;
   __syncthreads();
   // LDS values are wave-uniform: kept in scalar registers
