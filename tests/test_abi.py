@@ -74,7 +74,8 @@ def _decode_args(**over):
     (dict(block_size=8), NotImplementedError, "block_size"),
     (dict(s_active=17), NotImplementedError, "active tokens"),
     (dict(num_q_heads=128, num_kv_heads=1), NotImplementedError, "query columns"),
-    (dict(batch=1025), NotImplementedError, "1024"),
+    (dict(batch=1025, active_mask=0x10000), NotImplementedError, "1024"),
+    (dict(batch=1025, mask_mode=1, full_mask=0x10000), NotImplementedError, "1024"),
     (dict(k_cache=0x10004), ValueError, "aligned"),
     (dict(cache_dtype=N.DTYPE_F32), NotImplementedError, "cache dtype"),
     (dict(pos_ids=None), ValueError, "pos_ids"),
@@ -283,6 +284,17 @@ def test_gather_requires_the_pool_size():
     L = N.lib()
     with pytest.raises(ValueError, match="geometry"):
         N.check(L.mia_gather_kv(ctypes.byref(_gather_args(num_blocks=0)), None), "gather_kv")
+
+
+def test_decode_batch_beyond_one_launch_sequence():
+    """More than 1024 rows (position mask) run as consecutive row chunks
+    sharing one workspace: the workspace is that of the larger chunk plan
+    (a full chunk or the remainder)."""
+    L = N.lib()
+    big = L.mia_decode_workspace_bytes(ctypes.byref(_decode_args(batch=2500, blocks_per_seq=64)))
+    full = L.mia_decode_workspace_bytes(ctypes.byref(_decode_args(batch=1024, blocks_per_seq=64)))
+    rem = L.mia_decode_workspace_bytes(ctypes.byref(_decode_args(batch=452, blocks_per_seq=64)))
+    assert big == max(full, rem) > 0
 
 
 def test_noalloc_decode_rejects_plans_beyond_its_static_scratch():

@@ -538,3 +538,49 @@ def test_many_pieces_per_wave(gpu, kw):
     assert torch.isfinite(many).all()
     assert (many.double() - ref).abs().max().item() <= tol
     assert (few.double() - ref).abs().max().item() <= tol
+
+
+@pytest.mark.parametrize("ctx_hi,S,private", [(200, 1, False), (600, 2, False), (600, 1, True)])
+def test_batch_beyond_one_launch_sequence(gpu, ctx_hi, S, private):
+    """1100 rows, beyond the 1024 of one persistent launch, in one call: it
+    runs as two row chunks sharing one workspace.  The output equals two
+    calls on the row slices bit for bit (one-pass and split-K tables) and
+    float64 math on the rows around the chunk boundary.  The cache writes
+    equal one scatter of every row: in the reference order (every write
+    after every read: the chunks attend first, then one scatter) and with
+    private slots (each row writes its own active positions)."""
+    import dataclasses
+    from vllm_neuron_amd import _kernels as K
+    cfg = _small_cfg(batch=1100, q_heads=16, kv_heads=2, head_dim=128, block_size=32,
+                     ctx_lo=1, ctx_hi=ctx_hi, seed=77)
+    b = _make(cfg, gpu, S=S)
+    B, Hkv, bs = cfg.batch, cfg.kv_heads, cfg.block_size
+
+    def rows_of(lo, hi):
+        return dataclasses.replace(
+            b, q=b.q[lo:hi], k_new=b.k_new[lo:hi], v_new=b.v_new[lo:hi],
+            block_table=b.block_table[lo:hi], pos=b.pos[lo:hi],
+            start=None if b.start is None else b.start[lo:hi])
+
+    if private:
+        p = b.pos.long()
+        rows = torch.arange(B, device=gpu).view(B, 1)
+        slots = (b.block_table[rows, p // bs].long() * bs + p % bs).reshape(-1)
+    else:
+        g = torch.Generator().manual_seed(5)
+        slots = torch.randperm(b.k_cache.shape[0] * bs, generator=g)[:B * S].to(gpu)
+    ref = _fp32(rows_of(1000, B), cfg.head_dim ** -0.5)  # the untouched cache
+    kc, vc = b.k_cache.clone(), b.v_cache.clone()
+    whole = _run_core(b, write_slots=slots, write_slots_private=private)
+    torch.cuda.synchronize()
+    kw, vw = b.k_cache.clone(), b.v_cache.clone()
+    b.k_cache.copy_(kc)
+    b.v_cache.copy_(vc)
+    parts = torch.cat([_run_core(rows_of(0, 1024)), _run_core(rows_of(1024, B))])
+    K.kv_write(b.k_new.reshape(B * S, Hkv, -1), b.v_new.reshape(B * S, Hkv, -1), slots,
+               kc, vc)
+    torch.cuda.synchronize()
+    assert torch.equal(whole, parts)
+    assert (whole[1000:].float().cpu().double() - ref).abs().max().item() <= TOL_BF16
+    assert torch.equal(kw.view(torch.uint8), kc.view(torch.uint8))
+    assert torch.equal(vw.view(torch.uint8), vc.view(torch.uint8))

@@ -3,6 +3,7 @@
 // reporting and dispatch to the kernel launchers.
 #include <stdint.h>
 
+#include <algorithm>
 #include <cstdio>
 #include <string>
 
@@ -153,6 +154,59 @@ static int check_cache_layout(const char *err_dtype, const char *err_layout, int
   return MIA_OK;
 }
 
+// A decode batch above mia::kDecodeMaxRows rows (position mask only: a mask
+// tensor is indexed with the launch's own batch) runs as consecutive launch
+// sequences of at most that many rows on the stream, which share one
+// workspace (rows are independent).
+static constexpr int kDecodeRows = mia::kDecodeMaxRows;
+
+// The arguments of rows [b0, b0 + n) of a decode call.
+static mia_decode_args decode_rows(const mia_decode_args &a, int b0, int n) {
+  mia_decode_args c = a;
+  c.batch = n;
+  c.q = (const uint16_t *)a.q + (int64_t)b0 * a.q_stride[0];
+  c.k_new = (const uint16_t *)a.k_new + (int64_t)b0 * a.k_new_stride[0];
+  c.v_new = (const uint16_t *)a.v_new + (int64_t)b0 * a.v_new_stride[0];
+  c.block_table = a.block_table + (int64_t)b0 * a.bt_stride[0];
+  c.pos_ids = a.pos_ids ? a.pos_ids + (int64_t)b0 * a.s_active : nullptr;
+  c.start_pos = a.start_pos ? a.start_pos + (int64_t)b0 * a.s_active : nullptr;
+  c.out = (uint16_t *)a.out + (int64_t)b0 * a.out_stride[0];
+  if (a.write_slots)
+    c.write_slots = (const uint8_t *)a.write_slots +
+                    (int64_t)b0 * a.s_active * (a.write_slot_dtype == MIA_DTYPE_I64 ? 8 : 4);
+  c.split_event_begin = b0 == 0 ? a.split_event_begin : nullptr;
+  c.split_event_end = b0 + n == a.batch ? a.split_event_end : nullptr;
+  return c;
+}
+
+// Workspace of a (validated) decode call: the largest of its launch
+// sequences' plans (a full chunk of rows and the remainder).
+static size_t decode_ws_bytes(const mia_decode_args &a) {
+  if (a.batch <= kDecodeRows) return mia::plan_decode(a).ws_bytes;
+  size_t ws = mia::plan_decode(decode_rows(a, 0, kDecodeRows)).ws_bytes;
+  const int rem = a.batch % kDecodeRows;
+  if (rem) ws = std::max(ws, mia::plan_decode(decode_rows(a, a.batch - rem, rem)).ws_bytes);
+  return ws;
+}
+
+// Launches every row chunk of a validated call with workspace ws.  Cache
+// writes that are not private to their row are kept in the reference's
+// order (every write after every read): the chunks attend without them and
+// one scatter of all rows follows.
+static int launch_decode_rows(const mia_decode_args &a, void *ws, size_t ws_bytes,
+                              hipStream_t s) {
+  const bool defer = a.batch > kDecodeRows && a.write_slots && !a.write_private;
+  for (int b0 = 0; b0 < a.batch; b0 += kDecodeRows) {
+    mia_decode_args c = decode_rows(a, b0, std::min(kDecodeRows, a.batch - b0));
+    c.workspace = ws;
+    c.workspace_bytes = ws_bytes;
+    if (defer) c.write_slots = nullptr;
+    const int rc = mia::launch_paged_decode(c, mia::plan_decode(c), s);
+    if (rc) return rc;
+  }
+  return defer ? mia::launch_decode_scatter(a, s) : MIA_OK;
+}
+
 static int validate_decode(const mia_decode_args *a) {
   MIA_REQUIRE(a, MIA_ERR_VALUE, "decode: null args");
   MIA_REQUIRE(a->q && a->k_new && a->v_new && a->k_cache && a->v_cache &&
@@ -161,8 +215,10 @@ static int validate_decode(const mia_decode_args *a) {
   MIA_REQUIRE(a->batch > 0 && a->s_active > 0 && a->num_q_heads > 0 &&
                   a->num_kv_heads > 0,
               MIA_ERR_VALUE, "decode: bad shape");
-  MIA_REQUIRE(a->batch <= 1024, MIA_ERR_NOT_IMPLEMENTED,
-              "decode: at most 1024 batch rows per call");
+  MIA_REQUIRE(a->batch <= kDecodeRows || (a->mask_mode == 0 && a->active_mask == nullptr),
+              MIA_ERR_NOT_IMPLEMENTED,
+              "decode: more than 1024 batch rows per call need the position mask (no mask "
+              "tensor)");
   MIA_REQUIRE(a->num_q_heads % a->num_kv_heads == 0, MIA_ERR_VALUE,
               "GQA requires q_heads divisible by kv_heads");
   MIA_REQUIRE(a->head_dim == 64 || a->head_dim == 128, MIA_ERR_NOT_IMPLEMENTED,
@@ -181,7 +237,8 @@ static int validate_decode(const mia_decode_args *a) {
               "decode: context beyond 2^24 tokens");
   // the split kernel counts the 32-token tiles of all (row, kv head)
   // segments in 32-bit integers
-  MIA_REQUIRE((int64_t)a->batch * a->num_kv_heads * ((s_ctx + 31) / 32) < (1ll << 31),
+  MIA_REQUIRE((int64_t)std::min(a->batch, kDecodeRows) * a->num_kv_heads * ((s_ctx + 31) / 32) <
+                  (1ll << 31),
               MIA_ERR_VALUE, "decode: batch * kv_heads * context tiles beyond 2^31");
   const int G = a->num_q_heads / a->num_kv_heads;
   MIA_REQUIRE(G * a->s_active <= 64 && a->s_active <= 16,
@@ -220,6 +277,14 @@ static int validate_decode(const mia_decode_args *a) {
     MIA_REQUIRE(a->write_slot_dtype == MIA_DTYPE_I32 || a->write_slot_dtype == MIA_DTYPE_I64 ||
                     a->write_slot_dtype == MIA_DTYPE_U32,
                 MIA_ERR_VALUE, "decode: write slots must be i32, i64 or u32");
+    // beyond one launch sequence, shared-order writes are one scatter of the
+    // batch's active rows taken as one token sequence
+    MIA_REQUIRE(a->batch <= kDecodeRows || a->write_private ||
+                    (a->k_new_stride[0] == (int64_t)a->s_active * a->k_new_stride[1] &&
+                     a->v_new_stride[0] == (int64_t)a->s_active * a->v_new_stride[1]),
+                MIA_ERR_NOT_IMPLEMENTED,
+                "decode: more than 1024 batch rows with shared-order write slots need the "
+                "new K/V rows laid out as one token sequence");
   }
   return MIA_OK;
 }
@@ -227,37 +292,33 @@ static int validate_decode(const mia_decode_args *a) {
 size_t mia_decode_workspace_bytes(const mia_decode_args *a) {
   mia::g_last_error.clear();
   if (validate_decode(a) != MIA_OK) return 0;
-  return mia::plan_decode(*a).ws_bytes;
+  return decode_ws_bytes(*a);
 }
 
 int mia_paged_decode(const mia_decode_args *a, mia_stream_t stream) {
   mia::g_last_error.clear();
   int rc = validate_decode(a);
   if (rc) return rc;
-  mia::DecodePlan pl = mia::plan_decode(*a);
-  MIA_REQUIRE(a->workspace && a->workspace_bytes >= pl.ws_bytes, MIA_ERR_VALUE,
+  MIA_REQUIRE(a->workspace && a->workspace_bytes >= decode_ws_bytes(*a), MIA_ERR_VALUE,
               "decode: workspace too small (query mia_decode_workspace_bytes)");
   MIA_REQUIRE(aligned(a->workspace, 256), MIA_ERR_VALUE,
               "decode: workspace must be 256-byte aligned");
-  return mia::launch_paged_decode(*a, pl, (hipStream_t)stream);
+  return launch_decode_rows(*a, a->workspace, a->workspace_bytes, (hipStream_t)stream);
 }
 
 int mia_paged_decode_noalloc(const mia_decode_args *a, mia_stream_t stream) {
   mia::g_last_error.clear();
   int rc = validate_decode(a);
   if (rc) return rc;
-  const mia::DecodePlan pl = mia::plan_decode(*a);
-  MIA_REQUIRE(pl.ws_bytes <= MIA_DECODE_NOALLOC_SCRATCH_BYTES, MIA_ERR_VALUE,
-              "decode (no-alloc): the call needs " + std::to_string(pl.ws_bytes) +
+  const size_t need = decode_ws_bytes(*a);
+  MIA_REQUIRE(need <= MIA_DECODE_NOALLOC_SCRATCH_BYTES, MIA_ERR_VALUE,
+              "decode (no-alloc): the call needs " + std::to_string(need) +
                   " bytes of scratch, the static scratch holds " +
                   std::to_string((size_t)MIA_DECODE_NOALLOC_SCRATCH_BYTES));
   void *ws = nullptr;
   rc = mia::decode_noalloc_scratch(&ws);
   if (rc) return rc;
-  mia_decode_args b = *a;
-  b.workspace = ws;
-  b.workspace_bytes = MIA_DECODE_NOALLOC_SCRATCH_BYTES;
-  return mia::launch_paged_decode(b, pl, (hipStream_t)stream);
+  return launch_decode_rows(*a, ws, MIA_DECODE_NOALLOC_SCRATCH_BYTES, (hipStream_t)stream);
 }
 
 static int validate_prefill(const mia_prefill_args *a) {

@@ -45,11 +45,18 @@ struct DecodePlan {
   size_t ws_bytes;   // workspace bytes
 };
 DecodePlan plan_decode(const mia_decode_args &a);
+// Batch rows of one decode launch sequence at most (per-row tables of the
+// persistent split kernel live in LDS); the ABI layer runs larger batches as
+// consecutive row chunks.
+constexpr int kDecodeMaxRows = 1024;
 // Device address of the current device's static decode scratch
 // (MIA_DECODE_NOALLOC_SCRATCH_BYTES), looked up once per device.
 int decode_noalloc_scratch(void **ptr);
 int launch_paged_decode(const mia_decode_args &a, const DecodePlan &p,
                         hipStream_t s);
+// The active K/V rows of a decode call written to its write_slots by one
+// cache-write launch (the batch's rows as one token sequence, t = b * S + s).
+int launch_decode_scatter(const mia_decode_args &a, hipStream_t s);
 
 // Paged prefill: split-K plan shared by the workspace query and the launch.
 struct PrefillPlan {

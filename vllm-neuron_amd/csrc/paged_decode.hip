@@ -107,7 +107,7 @@ constexpr int kMaxDeviceCUs = 1024;  // the weighted prefix stays below 2^22
 static_assert(kMaxClassWeight * 2 * kMaxDeviceCUs * 4 < (1 << 22), "share_start exactness");
 static_assert(kClassWeightBf16[0] <= kMaxClassWeight && kClassWeightFp8[0] <= kMaxClassWeight,
               "weights are non-increasing, the first is the largest");
-constexpr int kMaxRows = 1024;         // batch rows of the persistent decode
+constexpr int kMaxRows = kDecodeMaxRows;  // batch rows of one persistent decode launch
 
 // Compute units of the current device (queried once per device).
 int device_cu_count() {
@@ -1507,6 +1507,38 @@ int decode_noalloc_scratch(void **ptr) {
 constexpr int kOnePassTiles = 8;
 constexpr int kOnePassTilesFew = 32;
 
+// The S active K/V rows of every batch row written to write_slots by the
+// cache-write kernel, the batch's active rows taken as one token sequence
+// (t = b * S + s: k_new / v_new rows must be laid out that way).
+int launch_decode_scatter(const mia_decode_args &a, hipStream_t s) {
+  mia_kv_write_args w{};
+  w.k_src = a.k_new;
+  w.v_src = a.v_new;
+  w.src_dtype = MIA_DTYPE_BF16;
+  for (int i = 0; i < 3; ++i) {
+    w.k_src_stride[i] = a.k_new_stride[i + 1];
+    w.v_src_stride[i] = a.v_new_stride[i + 1];
+  }
+  w.slots = a.write_slots;
+  w.slot_dtype = a.write_slot_dtype;
+  w.num_tokens = (int64_t)a.batch * a.s_active;
+  w.k_cache = (void *)a.k_cache;
+  w.v_cache = (void *)a.v_cache;
+  w.cache_dtype = a.cache_dtype;
+  w.k_packed = a.k_packed;
+  for (int i = 0; i < 5; ++i) w.k_cache_stride[i] = a.k_cache_stride[i];
+  for (int i = 0; i < 4; ++i) w.v_cache_stride[i] = a.v_cache_stride[i];
+  w.num_blocks = a.num_blocks;
+  w.block_size = a.block_size;
+  w.num_kv_heads = a.num_kv_heads;
+  w.head_dim = a.head_dim;
+  w.quant_mode = a.quant_mode;
+  w.scale_per_head = a.quant_per_head;
+  w.k_scale = a.k_quant;
+  w.v_scale = a.v_quant;
+  return launch_kv_write(w, s);
+}
+
 DecodePlan plan_decode(const mia_decode_args &a) {
   DecodePlan pl;
   const int G = a.num_q_heads / a.num_kv_heads;
@@ -1698,33 +1730,7 @@ int launch_paged_decode(const mia_decode_args &a, const DecodePlan &pl,
       if (rc) return rc;
     }
     if (!a.write_slots || fused_write) return MIA_OK;
-    // the active rows of the batch as one token sequence (t = b * S + s)
-    mia_kv_write_args w{};
-    w.k_src = a.k_new;
-    w.v_src = a.v_new;
-    w.src_dtype = MIA_DTYPE_BF16;
-    for (int i = 0; i < 3; ++i) {
-      w.k_src_stride[i] = a.k_new_stride[i + 1];
-      w.v_src_stride[i] = a.v_new_stride[i + 1];
-    }
-    w.slots = a.write_slots;
-    w.slot_dtype = a.write_slot_dtype;
-    w.num_tokens = (int64_t)a.batch * a.s_active;
-    w.k_cache = (void *)a.k_cache;
-    w.v_cache = (void *)a.v_cache;
-    w.cache_dtype = a.cache_dtype;
-    w.k_packed = a.k_packed;
-    for (int i = 0; i < 5; ++i) w.k_cache_stride[i] = a.k_cache_stride[i];
-    for (int i = 0; i < 4; ++i) w.v_cache_stride[i] = a.v_cache_stride[i];
-    w.num_blocks = a.num_blocks;
-    w.block_size = a.block_size;
-    w.num_kv_heads = a.num_kv_heads;
-    w.head_dim = a.head_dim;
-    w.quant_mode = a.quant_mode;
-    w.scale_per_head = a.quant_per_head;
-    w.k_scale = a.k_quant;
-    w.v_scale = a.v_quant;
-    return launch_kv_write(w, s);
+    return launch_decode_scatter(a, s);
   }
   const dim3 grid((unsigned)pl.grid);
   if (a.split_event_begin) {
