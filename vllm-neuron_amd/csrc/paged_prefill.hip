@@ -778,9 +778,8 @@ __global__ __launch_bounds__(256, 2) void prefill_kernel(PrefillKParams p) {
 // rows) per workgroup and the 64-key K and V tiles travelling HBM -> LDS
 // with global_load_lds_dwordx4 (no registers, no VALU) through a 3-stage
 // ring: tiles t+1 and t+2 are in flight while tile t is computed, one
-// barrier per tile.  The byte offsets of the blocks of the workgroup's key
-// range are staged in LDS once, so no global load sits between two tiles'
-// copies.
+// barrier per tile.  The blocks of the workgroup's key range are staged in
+// LDS once, so no global load sits between two tiles' copies.
 // A DMA instruction writes 64 lanes x 16 B contiguously, i.e. 4 rows of
 // 256 B; each lane picks which 16-byte chunk of its row it fetches, which
 // stores the rows XOR-swizzled:
@@ -835,9 +834,13 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   typedef __attribute__((address_space(3))) s16x4_t lds_s16x4_t;
   typedef __attribute__((address_space(3))) uint8_t lds_u8_t;
 
-  // byte offset of each block of the workgroup's key range (K and V share
-  // the block and token strides on this path)
-  __shared__ __attribute__((aligned(16))) int64_t offs_lds[kDmaIds];
+  // each block of the workgroup's key range (K and V share the block and
+  // token strides on this path): bf16, its byte offset; FP8, its block id
+  // (clamped into the pool), the copies forming the offset (measured: bf16
+  // 69.3 -> 69.9 us with ids on the 4 x 512 sub-batch, FP8 71.3 -> 70.0 us
+  // on the 2048-token chunk)
+  typedef std::conditional_t<FP8, int32_t, int64_t> blk_t;
+  __shared__ __attribute__((aligned(16))) blk_t ids_lds[kDmaIds];
   // bf16: [stage][K, V] tiles of the ring; FP8: [buffer][K, V] bf16 tiles
   // the products read, the FP8 ring in kv8_lds
   __shared__ __attribute__((aligned(1024))) uint8_t kv_lds[FP8 ? 2 : STAGES][2][TILEB];
@@ -849,8 +852,9 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
 
   // heaviest work item first (the block-id buffer is free until it is filled)
   SeqInfo si;
-  const uint3 tile = ranked_tile<WAVES * 64>(p, reinterpret_cast<int *>(offs_lds), 2 * kDmaIds, si);
-  __syncthreads();  // the ranking scratch is read before the block offsets land
+  const uint3 tile = ranked_tile<WAVES * 64>(p, reinterpret_cast<int *>(ids_lds),
+                                             kDmaIds * (int)(sizeof(blk_t) / 4), si);
+  __syncthreads();  // the ranking scratch is read before the blocks are staged
   const int sp = tile.z / p.num_seqs;  // key chunk of a split row tile
   const int seq = tile.z - sp * p.num_seqs;
   const int h = tile.y;
@@ -892,7 +896,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   // Q pre-multiplied by the softmax scale (log2 units) and rounded to bf16,
   // so that the MFMA yields scaled scores and the softmax needs no multiply
   const float scale2 = p.scale_log2 * (p.k_deq ? p.k_deq[h] : 1.0f);
-  // ---- byte offsets of blocks b_lo .. b_hi (ids clamped into the pool).
+  // ---- blocks b_lo .. b_hi staged in LDS (ids clamped into the pool).
   // The first block id of each thread is loaded before Q, so that the wait
   // for it leaves the Q loads in flight.
   const int64_t bt_row = (int64_t)seq * p.bt_s + (int64_t)h * p.bt_h;
@@ -900,9 +904,20 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   const int b_hi = min((int)fdiv((uint32_t)(kt_last + kKT - 1), p.bs_div), p.nblk - 1);
   const int n_blk = any_key ? b_hi - b_lo + 1 : 0;
   const int32_t bt0 = tid < n_blk ? p.bt[bt_row + (int64_t)(b_lo + tid) * p.bt_j] : 0;
-  auto blk_off = [&](int32_t v) {
+  auto blk_id = [&](int32_t v) -> blk_t {
     v = v < 0 ? 0 : (v >= p.nb ? p.nb - 1 : v);
-    return (int64_t)v * p.kc_blk * EB;
+    if constexpr (FP8) return v;
+    else return (int64_t)v * p.kc_blk * EB;
+  };
+  // byte offset of staged block bi (wave-uniform)
+  auto blk_off = [&](int bi) -> int64_t {
+    if constexpr (FP8) {
+      return (int64_t)readfirstlane(ids_lds[bi]) * p.kc_blk * EB;
+    } else {
+      const int64_t o = ids_lds[bi];
+      return (int64_t)(((uint64_t)(uint32_t)readfirstlane((int)(o >> 32)) << 32) |
+                       (uint32_t)readfirstlane((int)o));
+    }
   };
   // raw bf16 Q, loaded by every lane (rows past the sequence read token 0,
   // which exists: the launch returns early without tokens) and scaled once
@@ -915,9 +930,9 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
     for (int ks = 0; ks < KSTEPS; ++ks)
       qw[ks] = *reinterpret_cast<const u32x4_t *>(qp + ks * 16 + half * 8);
   }
-  if (tid < n_blk) offs_lds[tid] = blk_off(bt0);
+  if (tid < n_blk) ids_lds[tid] = blk_id(bt0);
   for (int i = tid + WAVES * 64; i < n_blk; i += WAVES * 64)
-    offs_lds[i] = blk_off(p.bt[bt_row + (int64_t)(b_lo + i) * p.bt_j]);
+    ids_lds[i] = blk_id(p.bt[bt_row + (int64_t)(b_lo + i) * p.bt_j]);
   // Q scaled and rounded after the first copies are issued (its wait then
   // overlaps theirs) and before the loop: a wait placed by the compiler
   // inside the loop would also drain the in-flight copies.  Rows that are
@@ -977,10 +992,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
     for (int j = 0; j < NJ; ++j) {
       const int q = kDmaWaves * j + wave;
       const int bi = min(kt_blk + jblk[j], p.nblk - 1) - b_lo;
-      const int64_t o = offs_lds[bi];
-      const int64_t off =
-          (int64_t)(((uint64_t)(uint32_t)readfirstlane((int)(o >> 32)) << 32) |
-                    (uint32_t)readfirstlane((int)o)) + ktb;
+      const int64_t off = blk_off(bi) + ktb;
       dma16(k_head + off + k_lane[j], k_dst + q * 1024);
       dma16(v_head + off + v_lane[j], v_dst + q * 1024);
     }
@@ -1091,10 +1103,7 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
         for (int j = 0; j < NJ8; ++j) {
           const int q = kDmaWaves * j + wave;
           const int bi = min(kt_blk + jblk8[j], p.nblk - 1) - b_lo;
-          const int64_t o = offs_lds[bi];
-          const int64_t off =
-              (int64_t)(((uint64_t)(uint32_t)readfirstlane((int)(o >> 32)) << 32) |
-                        (uint32_t)readfirstlane((int)o)) + ktb;
+          const int64_t off = blk_off(bi) + ktb;
           dma16(k_head + off + lane8[j], k_dst + q * 1024);
           dma16(v_head + off + lane8[j], v_dst + q * 1024);
         }
