@@ -837,8 +837,9 @@ __global__ __launch_bounds__(WAVES * 64, 8 / WAVES) void prefill_dma_kernel(Pref
   // each block of the workgroup's key range (K and V share the block and
   // token strides on this path): bf16, its byte offset; FP8, its block id
   // (clamped into the pool), the copies forming the offset (measured: bf16
-  // 69.3 -> 69.9 us with ids on the 4 x 512 sub-batch, FP8 71.3 -> 70.0 us
-  // on the 2048-token chunk)
+  // 69.3 -> 69.9 us with ids on the 4 x 512 sub-batch and 236.7 -> 237.7 us
+  // on the mixed batch's compact launch, FP8 71.3 -> 70.0 us on the
+  // 2048-token chunk)
   typedef std::conditional_t<FP8, int32_t, int64_t> blk_t;
   __shared__ __attribute__((aligned(16))) blk_t ids_lds[kDmaIds];
   // bf16: [stage][K, V] tiles of the ring; FP8: [buffer][K, V] bf16 tiles
