@@ -12,8 +12,9 @@
 //   covers every query column of its GQA group (column = query token s x
 //   head g, up to 16 per launch), so each K/V byte is read from HBM once.
 //   Every workgroup first computes each row's attended range and the tile
-//   prefix sum in LDS (rows <= 1024); a wave maps a tile to its segment by
-//   binary search.
+//   prefix sum in LDS (at most 1024 rows per launch: larger batches run as
+//   consecutive row chunks); a wave maps a tile to its segment by binary
+//   search.
 //
 // Per 32-token tile and wave
 //   K  : 2 sub-tiles of 16 tokens loaded straight into MFMA A-operand
