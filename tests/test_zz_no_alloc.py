@@ -34,11 +34,11 @@ def _decode(b, cfg, no_alloc):
 ])
 def test_noalloc_decode_equals_workspace_decode(names):
     dev = torch.device("cuda:0")
-    configs = dict(W.DECODE_CONFIGS)
-    configs["small_b3"] = W.DecodeConfig("small_b3", 3, 32, 8, 128, 32, 40, 900, sink=True,
+    cases = dict(W.DECODE_CONFIGS)
+    cases["small_b3"] = W.DecodeConfig("small_b3", 3, 32, 8, 128, 32, 40, 900, sink=True,
                                          seed=77)
     for name in names:
-        cfg = configs[name]
+        cfg = cases[name]
         print(f"no-alloc decode: {name}", flush=True)
         b = W.make_decode_batch(cfg, dev)
         ref = _decode(b, cfg, no_alloc=False)
