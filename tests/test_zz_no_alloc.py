@@ -36,7 +36,7 @@ def test_noalloc_decode_equals_workspace_decode(names):
     dev = torch.device("cuda:0")
     cases = dict(W.DECODE_CONFIGS)
     cases["small_b3"] = W.DecodeConfig("small_b3", 3, 32, 8, 128, 32, 40, 900, sink=True,
-                                         seed=77)
+                                       seed=77)
     for name in names:
         cfg = cases[name]
         print(f"no-alloc decode: {name}", flush=True)
