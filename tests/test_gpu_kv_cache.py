@@ -93,6 +93,32 @@ def test_kv_write_fp8_bit_exact(gpu, mode, per_head):
     assert torch.equal(_bytes(vcd), _bytes(vc))
 
 
+@pytest.mark.parametrize("geom", [(37, 3, 24, 80), (50, 6, 16, 136), (9, 8, 64, 128)])
+@pytest.mark.parametrize("slot_dtype", [torch.int64, torch.int32])
+def test_kv_write_vector_path_uneven_geometry(gpu, geom, slot_dtype):
+    """The vector kernel splits chunk, row and slot indices by multiplies for
+    the chunk count per row (head_dim / 8), the kv heads and the block size:
+    divisors that are not powers of two, a last workgroup only partly full
+    and sentinels on both sides of the pool land bit-exact."""
+    nb, H, bs, d = geom
+    g = torch.Generator().manual_seed(nb + H + bs + d)
+    T = min(nb * bs - 2, 301)
+    kc = torch.randn((nb, H, bs, d), generator=g).to(torch.bfloat16)
+    vc = torch.randn((nb, H, bs, d), generator=g).to(torch.bfloat16)
+    k = torch.randn((T, H, d), generator=g).to(torch.bfloat16)
+    v = torch.randn((T, H, d), generator=g).to(torch.bfloat16)
+    slots = torch.randperm(nb * bs, generator=g)[:T]
+    slots[0] = nb * bs - 1  # last slot of the pool
+    slots[1] = -1
+    slots[T - 1] = nb * bs  # first slot past the pool
+    kcd, vcd = kc.to(gpu), vc.to(gpu)
+    K.kv_write(k.to(gpu), v.to(gpu), slots.to(slot_dtype).to(gpu), kcd, vcd)
+    _index_put_ref(kc, k, slots, bs)
+    _index_put_ref(vc, v, slots, bs)
+    assert torch.equal(_bytes(kcd), _bytes(kc))
+    assert torch.equal(_bytes(vcd), _bytes(vc))
+
+
 @pytest.mark.parametrize("fp8", [False, True])
 def test_kv_write_vector_and_element_paths_agree(gpu, fp8):
     """Contiguous bf16 rows take the 8-element vector kernel; the same values
