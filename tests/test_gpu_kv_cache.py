@@ -107,7 +107,7 @@ def test_kv_write_vector_path_uneven_geometry(gpu, geom, slot_dtype):
     vc = torch.randn((nb, H, bs, d), generator=g).to(torch.bfloat16)
     k = torch.randn((T, H, d), generator=g).to(torch.bfloat16)
     v = torch.randn((T, H, d), generator=g).to(torch.bfloat16)
-    slots = torch.randperm(nb * bs, generator=g)[:T]
+    slots = torch.randperm(nb * bs - 1, generator=g)[:T]  # distinct, last slot left out
     slots[0] = nb * bs - 1  # last slot of the pool
     slots[1] = -1
     slots[T - 1] = nb * bs  # first slot past the pool
