@@ -9,6 +9,8 @@
 * a HIP graph capturing the decode (with its fused cache write) and the
   prefill replays several times, with unrelated eager work and host
   synchronisation between replays, each replay equal to the eager result;
+  so does the mixed batch, whose graph runs its decode and prefill halves
+  concurrently while the eager call runs them one after the other;
   graphs of the other drop-ins replay equal to eager calls after the
   device scalars they read (prior length, prior_used_len, cp_offset) are
   changed between replays, which shows that none was read on the host at
@@ -317,3 +319,43 @@ def test_hip_graph_segmented_and_qkv_proj_replay_equal_eager(gpu):
         torch.cuda.synchronize()
         assert torch.equal(out_s, ref_s), f"segmented, prior {p}"
         assert torch.equal(out_q, ref_q) and torch.equal(qa["kc"], kc_ref)
+
+
+def test_hip_graph_mixed_batch_overlapped_replays_equal_eager(gpu):
+    """The Llama-3-8B mixed batch captured into a HIP graph, where its halves
+    run concurrently (the decode on a side stream forked from and joined to
+    the capturing stream, the prefill with the compact launch), replays
+    equal to the eager call, which runs the halves one after the other with
+    the 8-wave prefill launch: both launches give a row the same products in
+    the same order and the same key chunks, so the outputs are equal bit for
+    bit, and so is the cache (prefill rows written before their attention,
+    decode rows after).  Four replays with eager work and host
+    synchronisation between them."""
+    from vllm_neuron_amd.functional import mixed_batch_attention
+
+    m = W.make_mixed_batch(gpu)
+    db, pb = m.decode, m.prefill
+
+    def work():
+        return mixed_batch_attention(
+            m.k_cache, m.v_cache, q_decode=db.q, k_decode=db.k_new, v_decode=db.v_new,
+            decode_block_table=db.block_table, decode_pos_ids=db.pos, decode_slots=db.slots,
+            q_prefill=pb.q, k_prefill=pb.k_new, v_prefill=pb.v_new, prefill_slots=pb.slots,
+            prefill_cu_seqlens=pb.cu_seqlens, prefill_prior=pb.prior,
+            prefill_block_table=pb.block_table, max_seqlen_q=pb.max_seqlen_q)
+
+    ref_d, ref_p = (t.clone() for t in work())  # eager: serial halves
+    torch.cuda.synchronize()
+    kc_ref, vc_ref = m.k_cache.clone(), m.v_cache.clone()
+    graph, (out_d, out_p) = _capture(work)
+    for i in range(4):
+        out_d.zero_()
+        out_p.zero_()
+        noise = torch.randn(1 << 20, device=gpu).sum()  # unrelated eager work
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(noise)
+        assert torch.equal(out_d, ref_d), f"replay {i}: decode rows differ"
+        assert torch.equal(out_p, ref_p), f"replay {i}: prefill rows differ"
+        assert torch.equal(m.k_cache, kc_ref) and torch.equal(m.v_cache, vc_ref), \
+            f"replay {i}: cache differs"
