@@ -4,6 +4,8 @@ against the workspace one (``mia_paged_decode``), through the C ABI.
 Both run the same kernels on the same plan, so their outputs must be equal
 bit for bit.  Two calls in a row, the second on a smaller batch: the static
 scratch keeps the first call's contents, which the second must not read.
+A HIP graph of the allocation-free call replays equal to the workspace
+path with an eager allocation-free call between replays.
 """
 import pytest
 import torch
@@ -79,3 +81,42 @@ def test_noalloc_one_pass_shape_with_a_large_split_layout():
         torch.cuda.synchronize()
         assert torch.isfinite(got.float()).all()
         assert torch.equal(got, ref), f"B={B}: no-alloc output differs"
+
+
+def test_noalloc_decode_graph_replays_equal_workspace_decode():
+    """Captured into a HIP graph (the callers the entry point is for), the
+    allocation-free decode of the full Llama-3-8B shape replays equal to the
+    workspace path; before each replay an eager allocation-free call of a
+    3-row batch overwrites the shared static scratch, which the replay must
+    not depend on."""
+    dev = torch.device("cuda:0")
+    cfg = W.DECODE_CONFIGS["llama3_8b_decode_b64"]
+    small = W.DecodeConfig("small_b3", 3, 32, 8, 128, 32, 40, 900, sink=True, seed=77)
+    b = W.make_decode_batch(cfg, dev)
+    bs = W.make_decode_batch(small, dev)
+    ref = _decode(b, cfg, no_alloc=False)
+    ref_small = _decode(bs, small, no_alloc=False)
+    out = torch.empty_like(b.q)
+
+    def work():
+        K.paged_decode(b.q, b.k_new, b.v_new, b.k_cache, b.v_cache, b.block_table,
+                       softmax_scale=cfg.head_dim ** -0.5, pos_ids=b.pos, start_pos=b.start,
+                       sink=b.sink, out=out, no_alloc=True)
+
+    side = torch.cuda.Stream(device=dev)
+    side.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(side):  # warm-up outside the capture
+        work()
+    torch.cuda.current_stream(dev).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        work()
+    for i in range(3):
+        out.zero_()
+        print(f"no-alloc graph replay {i}", flush=True)
+        got_small = _decode(bs, small, no_alloc=True)  # eager, same scratch
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(got_small, ref_small), f"replay {i}: eager 3-row call differs"
+        assert torch.equal(out, ref), f"replay {i}: captured call differs"
