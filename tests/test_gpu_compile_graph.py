@@ -9,8 +9,9 @@
 * a HIP graph capturing the decode (with its fused cache write) and the
   prefill replays several times, with unrelated eager work and host
   synchronisation between replays, each replay equal to the eager result;
-  so does the mixed batch, whose graph runs its decode and prefill halves
-  concurrently while the eager call runs them one after the other;
+  so does the mixed batch (bf16 and FP8 caches), whose graph runs its
+  decode and prefill halves concurrently while the eager call runs them one
+  after the other;
   graphs of the other drop-ins replay equal to eager calls after the
   device scalars they read (prior length, prior_used_len, cp_offset) are
   changed between replays, which shows that none was read on the host at
@@ -359,3 +360,52 @@ def test_hip_graph_mixed_batch_overlapped_replays_equal_eager(gpu):
         assert torch.equal(out_p, ref_p), f"replay {i}: prefill rows differ"
         assert torch.equal(m.k_cache, kc_ref) and torch.equal(m.v_cache, vc_ref), \
             f"replay {i}: cache differs"
+
+
+def test_hip_graph_fp8_mixed_batch_replays_equal_eager(gpu):
+    """An FP8 mixed batch (per-kv-head scales: the prefill rows quantised on
+    their write, the decode rows' write fused into the decode merge) in a
+    HIP graph, where its halves overlap and the prefill takes the compact
+    launch's path for FP8 caches (the register-staged kernel), replays equal
+    to the eager call, which runs the halves serially with the copy-ring
+    kernel: on unsplit rows both kernels form the same products in the same
+    order.  Outputs and cache bytes, four replays."""
+    from vllm_neuron_amd.functional import mixed_batch_attention
+
+    # one seed: both builders draw the same per-head scales
+    pcfg = W.PrefillConfig("mp8", 2, 16, 2, 128, 32, 96, 0, 300, fp8=True, seed=85)
+    dcfg = W.DecodeConfig("md8", 3, 16, 2, 128, 32, 40, 500, fp8=True, seed=85)
+    pb = W.make_prefill_batch(pcfg, gpu)
+    db = W.make_decode_batch(dcfg, gpu)
+    assert torch.equal(pb.k_dequant, db.k_dequant) and torch.equal(pb.v_dequant, db.v_dequant)
+    nb_p = pb.k_cache.shape[0]
+    kc = torch.cat([pb.k_cache, db.k_cache], 0)
+    vc = torch.cat([pb.v_cache, db.v_cache], 0)
+    dt = torch.where(db.block_table >= 0, db.block_table + nb_p, db.block_table)
+    dslots = db.slots + nb_p * dcfg.block_size
+
+    def work():
+        return mixed_batch_attention(
+            kc, vc, q_decode=db.q, k_decode=db.k_new, v_decode=db.v_new, decode_block_table=dt,
+            decode_pos_ids=db.pos, decode_slots=dslots, q_prefill=pb.q, k_prefill=pb.k_new,
+            v_prefill=pb.v_new, prefill_slots=pb.slots, prefill_cu_seqlens=pb.cu_seqlens,
+            prefill_prior=pb.prior, prefill_block_table=pb.block_table,
+            max_seqlen_q=pb.max_seqlen_q, k_scale=pb.k_quant, v_scale=pb.v_quant,
+            k_dequant_scale=pb.k_dequant, v_dequant_scale=pb.v_dequant)
+
+    ref_d, ref_p = (t.clone() for t in work())  # eager: serial halves
+    torch.cuda.synchronize()
+    kc_ref, vc_ref = kc.clone(), vc.clone()
+    graph, (out_d, out_p) = _capture(work)
+    for i in range(4):
+        out_d.zero_()
+        out_p.zero_()
+        noise = torch.randn(1 << 20, device=gpu).sum()  # unrelated eager work
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(noise) and torch.isfinite(out_p.float()).all()
+        assert torch.equal(out_d, ref_d), f"replay {i}: decode rows differ"
+        dp = (out_p.float() - ref_p.float()).abs().max().item()
+        assert torch.equal(out_p, ref_p), f"replay {i}: prefill rows differ (max {dp})"
+        assert torch.equal(kc.view(torch.uint8), kc_ref.view(torch.uint8)) and \
+            torch.equal(vc.view(torch.uint8), vc_ref.view(torch.uint8)), f"replay {i}: cache differs"
